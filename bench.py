@@ -1,0 +1,242 @@
+"""Throughput of the bitsqz_llm compress + decompress hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A step is one device-resident compress (bsq_device_compress) followed by one
+device-resident decompress (bsq_device_decompress) of a synthetic FP32
+matrix that is already in HBM; `value` is GB/s of FP32 input
+(4*rows*cols*K / time of the K timed steps).  Prints one JSON line with the
+roofline figure of the dominant kernel (timed live with HIP events on the
+runtime stream) and the reference's CPU codec timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "bitsqueeze-llm_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import bitsqz_amd as B  # noqa: E402
+
+METRIC = "compress+decompress GB/s (FP32 in) at 4096×11008; % HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+# name -> (rows, cols, outlier ratio, error ratio, svd_ranks, svd_niters, uv, s, direct, generator)
+WORKLOADS = {
+    # BASELINE headline: 4096x11008 low-rank + noise + outlier columns with config-4 knobs
+    "headline": (4096, 11008, 0.005, 0.01, 256, 2, B.NF4, B.QUANT_NONE, B.QUANT_NONE, "lowrank"),
+    # the same matrix through the direct path (NF4_DQ + outlier + error top-k)
+    "direct_full": (4096, 11008, 0.005, 0.01, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4_DQ, "lowrank"),
+    "supplement": (4096, 11008, 0.0, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, "normal"),
+    "c1": (2048, 4096, 0.0, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, "normal"),
+    "c2": (4096, 4096, 0.005, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4_DQ, "outlier_cols"),
+}
+
+
+def make_input(rows, cols, gen, seed=0):
+    rng = np.random.default_rng(seed)
+    if gen == "normal":
+        return rng.standard_normal((rows, cols), dtype=np.float32)
+    if gen == "outlier_cols":
+        x = rng.standard_normal((rows, cols), dtype=np.float32)
+        x[:, np.random.default_rng(1).permutation(cols)[:16]] *= 60.0
+        return x
+    # low-rank A diag(sigma) B^T (rank 512, sigma_i = i^-1.2) + N(0, 0.01^2) + 8 columns x50
+    r = 512
+    A = rng.standard_normal((rows, r), dtype=np.float32)
+    Bm = np.random.default_rng(seed + 1).standard_normal((cols, r), dtype=np.float32)
+    sig = (np.arange(1, r + 1, dtype=np.float32) ** np.float32(-1.2)).astype(np.float32)
+    x = (A * sig[None, :]) @ Bm.T
+    x += np.float32(0.01) * np.random.default_rng(seed + 2).standard_normal((rows, cols), dtype=np.float32)
+    x[:, np.random.default_rng(seed + 3).permutation(cols)[:8]] *= 50.0
+    return np.ascontiguousarray(x, np.float32)
+
+
+def packed_payload_bytes(p: B.DevicePacked, err_present: bool) -> int:
+    h = p.header
+    total = 0
+    for name in ("section_u", "section_s", "section_v", "section_direct", "section_outlier_topk"):
+        s = getattr(h, name)
+        if s.storage:
+            total += s.size
+    if err_present and h.section_error_topk.storage:
+        total += h.section_error_topk.size
+    return total
+
+
+def time_dominant_kernel(wl, rows, cols, dsrc, stream, reps=20):
+    """Average duration (HIP events on the runtime stream) and algorithmic
+    bytes of the direct path's NF4/NF4_DQ encode of the full matrix, the
+    kernel that carries the direct-path traffic (read 4N, write the section)."""
+    _, _, ro, re, svd, _, uv, s, direct, _ = wl
+    n = rows * cols
+    method = direct if direct != B.QUANT_NONE else B.NF4
+    nb = (n + 63) // 64
+    scales_f = B.DeviceBuffer(nb * 4)
+    scales_u = B.DeviceBuffer(nb)
+    dq = B.DeviceBuffer(4)
+    codes = B.DeviceBuffer((n + 1) // 2)
+    L = B.lib()
+    for _ in range(3):
+        B.check(L.bsq_quant_compress(dsrc.ptr, n, method, scales_f.ptr, scales_u.ptr, dq.ptr, codes.ptr, stream),
+                "quant")
+    e0, e1 = B.Event(), B.Event()
+    e0.record(stream)
+    for _ in range(reps):
+        B.check(L.bsq_quant_compress(dsrc.ptr, n, method, scales_f.ptr, scales_u.ptr, dq.ptr, codes.ptr, stream),
+                "quant")
+    e1.record(stream)
+    ms = e0.elapsed_ms(e1) / reps
+    section = (nb * 4 if method == B.NF4 else nb) + (n + 1) // 2
+    alg_bytes = 4 * n + section
+    name = "quant_encode_kernel<NF4>" if method == B.NF4 else "dq_gmax_kernel + quant_encode_kernel<NF4_DQ>"
+    return name, ms, alg_bytes
+
+
+def cpu_baseline(x, direct, budget_s=12.0):
+    """The reference's legacy OpenMP NF4 / NF4_DQ codec (compiled from the
+    reference's own sources into oracle/_ref) on a bounded row sample of the
+    same matrix; falls back to the repository's C restatement (kind 'port')
+    when that library is absent."""
+    import ctypes
+
+    from oracle import oracle as O
+
+    method = direct if direct != B.QUANT_NONE else B.NF4
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libref_nf4.so")
+    rows = max(64, min(x.shape[0], 512))
+    sample = np.ascontiguousarray(x[:rows])
+    n = sample.size
+    nb, nc = (n + 63) // 64, (n + 1) // 2
+    out = np.empty(n, np.float32)
+    codes = np.empty(nc, np.uint8)
+    P = ctypes.c_void_p
+    if os.path.exists(ref_so):
+        L = ctypes.CDLL(ref_so)
+        kind = "reference"
+        if method == B.NF4:
+            L.ref_nf4_compress.argtypes = [P, ctypes.c_ulonglong, P, P]
+            L.ref_nf4_decompress.argtypes = [P, P, ctypes.c_ulonglong, P]
+            sc = np.empty(nb, np.float32)
+
+            def once():
+                L.ref_nf4_compress(sample.ctypes.data, n, sc.ctypes.data, codes.ctypes.data)
+                L.ref_nf4_decompress(sc.ctypes.data, codes.ctypes.data, n, out.ctypes.data)
+        else:
+            L.ref_nf4dq_compress.argtypes = [P, ctypes.c_ulonglong, P, P, P]
+            L.ref_nf4dq_decompress.argtypes = [ctypes.c_float, P, P, ctypes.c_ulonglong, P]
+            sc = np.empty(nb, np.uint8)
+            dq = np.zeros(1, np.float32)
+
+            def once():
+                L.ref_nf4dq_compress(sample.ctypes.data, n, dq.ctypes.data, sc.ctypes.data, codes.ctypes.data)
+                L.ref_nf4dq_decompress(ctypes.c_float(dq[0]), sc.ctypes.data, codes.ctypes.data, n,
+                                       out.ctypes.data)
+    else:
+        kind = "port"
+
+        def once():
+            q = O.quant_compress(sample, method)
+            O.quant_decompress(q)
+    once()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        once()
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= 200:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    gbs = 4 * n / dt / 1e9
+    label = "NF4" if method == B.NF4 else "NF4_DQ"
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"legacy {label} compress+decompress of the first {rows} rows ({rows}x{x.shape[1]}), "
+                      f"{reps} reps in {reps * dt:.1f} s; the reference has no CPU top-k / SVD path"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="headline", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only; the multi-GPU design (row shards, one "
+              "all-reduce per NF4_DQ section and per power iteration) is described in DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    wl = WORKLOADS[args.workload]
+    rows, cols, ro, re, svd, nit, uv, s, direct, gen = wl
+    x = make_input(rows, cols, gen)
+    print(f"bench: workload={args.workload} {rows}x{cols} generated", file=sys.stderr, flush=True)
+    B.compress_release()
+    B.decompress_release()
+    B.check(B.compress_initialize(rows, cols, ro, re, svd, nit, uv, s, direct, B.INPUT_DEVICE), "compress init")
+    q = max(1, min(svd, rows, cols)) if svd >= 1 else -1
+    B.check(B.decompress_initialize(rows, cols, ro, re, q, uv, s, direct), "decompress init")
+    dsrc = B.DeviceBuffer.from_array(x)
+    ddst = B.DeviceBuffer(x.nbytes)
+    n = rows * cols
+
+    def step():
+        p = B.device_compress(dsrc)
+        B.device_decompress(p, ddst, n)
+        return p
+
+    for _ in range(args.warmup):
+        p = step()
+    B.device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        p = step()
+    B.device_synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt / args.steps * 1e3
+    value = 4.0 * n * args.steps / dt / 1e9
+    print(f"bench: timed {args.steps} steps, {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    # correctness spot check of the last step against the input (reconstruction error)
+    out = ddst.download(np.float32, n).reshape(rows, cols)
+    rel = float(np.linalg.norm(out - x) / max(np.linalg.norm(x), 1e-30))
+
+    stream = B.runtime_stream()
+    kname, kms, kbytes = time_dominant_kernel(wl, rows, cols, dsrc, stream)
+    achieved = kbytes / (kms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kname,
+                "avg_ms": round(kms, 5), "alg_bytes": kbytes}
+
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": args.workload, "rows": rows, "cols": cols, "outlier_topk_ratio": ro,
+                   "error_correction_topk_ratio": re, "svd_ranks": svd, "svd_niters": nit,
+                   "svd_uv_format": uv, "svd_s_format": s, "quantization_only_format": direct,
+                   "input": "device-resident", "rel_frobenius_error": round(rel, 6)},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(x, direct if svd < 1 else uv)
+    B.compress_release()
+    B.decompress_release()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,156 @@
+// Internal declarations shared by the HIP kernels and the host runtime of the
+// MI355X (gfx950) bitsqz_llm library.  Nothing here is part of the public ABI
+// (include/bitsqz_llm.hpp, include/bitsqz_llm_c.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace bsq {
+
+// ---------------------------------------------------------------------------
+// constants of the packed format (reference
+// modules/quantization_cuda/include/quantization_cuda/quantization_cuda.cuh:10-13,
+// src/bitsqz_llm.cu:25-29)
+// ---------------------------------------------------------------------------
+constexpr uint64_t kQuantBlock = 64;
+constexpr float kE4M3Max = 448.0f;
+constexpr uint32_t kQuantMagic = 0x51544355u;
+constexpr uint16_t kQuantVersion = 1u;
+constexpr int kMethodNF4DQ = 10;
+constexpr int kMethodNF4 = 11;
+constexpr int kMethodNone = -1;
+
+constexpr uint32_t kFlagSvd = 1u << 0;
+constexpr uint32_t kFlagOutlier = 1u << 1;
+constexpr uint32_t kFlagError = 1u << 2;
+
+// Exact decision thresholds of the NF4 nearest-code search.  For a finite v
+// with |v| < 2 the reference's linear scan (first index minimising
+// |fl(v - L[i])|, quantization_cuda.cu:43-58) returns #{c : v >= kNF4Thr[c]}.
+// Each threshold is the smallest float at which the scan moves from code c to
+// c + 1; they were found by bisection over float bit patterns and the identity
+// is checked over every float with |v| < 2 by the CPU test suite.
+#define BSQ_NF4_THRESHOLDS                                                          \
+    {-0.848096371f, -0.610632896f, -0.45999524f, -0.33967942f, -0.234607399f,      \
+     -0.137911722f, -0.0455250144f, 0.0397901535f, 0.120255254f, 0.203521267f,     \
+     0.292013794f, 0.389312565f, 0.501663446f, 0.64278698f, 0.861478448f}
+#define BSQ_NF4_THRESHOLD_BITS                                                      \
+    {0xbf591cd8u, 0xbf1c5270u, 0xbeeb847fu, 0xbeadea76u, 0xbe703cecu, 0xbe0d38bbu,  \
+     0xbd3a7870u, 0x3d22fb00u, 0x3df64863u, 0x3e5067e1u, 0x3e9582d5u, 0x3ec753fau,  \
+     0x3f006d04u, 0x3f248db0u, 0x3f5c89dau}
+
+// NF4 code book (reference quantization_cuda.cu:20-37).
+#define BSQ_NF4_LEVELS                                                              \
+    {-1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,     \
+     -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,    \
+     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,             \
+     0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,              \
+     0.7229568362236023f, 1.0f}
+
+// ---------------------------------------------------------------------------
+// error handling: internal code throws, the ABI layer catches
+// ---------------------------------------------------------------------------
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] void fail(const std::string &msg);
+void hip_check(hipError_t e, const char *what);
+
+#define BSQ_HIP(call) ::bsq::hip_check((call), #call)
+#define BSQ_REQUIRE(cond, msg)            \
+    do {                                  \
+        if (!(cond)) ::bsq::fail(msg);    \
+    } while (0)
+
+__host__ __device__ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// kernel launchers (all asynchronous on `stream`)
+// ---------------------------------------------------------------------------
+
+// NF4 (method 11): scales_f32[ceil(n/64)], codes[ceil(n/2)].
+// NF4_DQ (method 10): scales_u8[ceil(n/64)], *dq_out, codes; `gmax_scratch`
+// is one device uint32 used for the global maximum.
+void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f32,
+                         uint8_t *scales_u8, float *dq_out, uint8_t *codes,
+                         uint32_t *gmax_scratch, hipStream_t stream);
+void launch_quant_decode(uint64_t n, int method, const float *scales_f32,
+                         const uint8_t *scales_u8, const float *dq, const uint8_t *codes,
+                         float *out, hipStream_t stream);
+void launch_nf4_code_batch(const float *v, uint64_t n, uint8_t *codes, hipStream_t stream);
+void launch_e4m3_encode_batch(const float *v, uint64_t n, uint8_t *codes, hipStream_t stream);
+void launch_e4m3_decode_batch(const uint8_t *c, uint64_t n, float *v, hipStream_t stream);
+// Histogram (16 bins) + checksum sum(code * (bits % 65521)) of the NF4 code of
+// every float bit pattern in [lo, hi).
+void launch_nf4_code_sweep(uint64_t lo, uint64_t hi, unsigned long long *hist16,
+                           unsigned long long *checksum, hipStream_t stream);
+
+// Top-k.  Value sources for the per-row selection.
+enum class TopkSource : int {
+    Dense = 0,        // v = a[r, c]
+    DenseMinusNF4 = 1,  // v = a[r, c] - dequant_nf4(...)[r, c]
+    DenseMinusNF4DQ = 2,
+    DenseMinusDense = 3,  // v = a[r, c] - b[r, c]
+};
+struct TopkArgs {
+    const float *a = nullptr;         // row-major rows x cols
+    const float *b = nullptr;         // DenseMinusDense subtrahend
+    const float *scales_f32 = nullptr;  // NF4 block scales of the subtrahend
+    const uint8_t *scales_u8 = nullptr; // NF4_DQ block scale codes
+    const float *dq = nullptr;          // NF4_DQ global scale
+    const uint8_t *codes = nullptr;     // packed nibbles of the subtrahend
+    uint32_t rows = 0, cols = 0, k = 0;
+    uint16_t *indices = nullptr;      // rows x k
+    float *values = nullptr;          // rows x k
+    float *residual = nullptr;        // optional: a with the selected entries zeroed
+    uint32_t *flags = nullptr;        // optional: OR kFlagError if any |v| > FLT_EPSILON
+    TopkSource source = TopkSource::Dense;
+};
+void launch_topk_select(const TopkArgs &args, hipStream_t stream);
+// Largest k the single-pass LDS sort handles.
+constexpr uint32_t kTopkMaxK = 8192;
+
+// dense[r, idx[r*k + j]] (+)= val[r*k + j]; with two lists, list 0 is applied
+// before list 1 row by row (the reference applies the error set, then the
+// outlier set).  When `gate0` is not null, list 0 is applied only if the
+// device word *gate0 has kFlagError set.
+void launch_topk_scatter(const uint16_t *idx0, const float *val0, uint32_t k0,
+                         const uint16_t *idx1, const float *val1, uint32_t k1, uint32_t rows,
+                         uint32_t cols, float *dense, bool accumulate, hipStream_t stream,
+                         const uint32_t *gate0 = nullptr);
+
+}  // namespace bsq
+
+namespace bsq {
+
+// ---------------------------------------------------------------------------
+// randomised low-rank SVD and reconstruction
+// ---------------------------------------------------------------------------
+struct SvdPlan;
+// Workspace for rank-q SVD of a row-major m x n matrix with `niter` power
+// iterations (q is clamped to [1, min(m, n)]).
+SvdPlan *svd_plan_create(int m, int n, int q, int niter);
+void svd_plan_destroy(SvdPlan *plan) noexcept;
+int svd_plan_rank(const SvdPlan *plan);
+// U (m x q), S (q), V (n x q), all row-major.  `sketch` (min(m,n) x q,
+// row-major, device) replaces the built-in Gaussian sketch when not null.
+void svd_run(SvdPlan *plan, const float *A, const float *sketch, uint64_t seed, float *U, float *S, float *V,
+             hipStream_t stream);
+// out = U diag(S) V^T (m x n row-major), or minuend - U diag(S) V^T when
+// `minuend` is not null.
+void launch_reconstruct(const float *U, const float *S, const float *V, int m, int n, int k,
+                        const float *minuend, float *out, hipStream_t stream);
+// N(0, 1) draws: Philox4x32-10 counter-based generator + Box-Muller.
+void launch_gaussian_fill(float *out, uint64_t n, uint64_t seed, hipStream_t stream);
+
+int cu_count();
+
+}  // namespace bsq

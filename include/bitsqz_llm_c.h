@@ -91,12 +91,15 @@ BSQ_API int bsq_compress_set_sketch(const float *d_sketch);
  * ------------------------------------------------------------------------- */
 
 /* A packed object whose sections live in device memory.  `header` carries the
- * exact header fields the host object would have (section offsets/sizes are
- * payload-relative, `payload` is NULL), except that the presence of the
- * error-correction section is decided on the device: *d_flags (device
- * memory) holds the final flags word.  The component pointers are device
- * pointers owned by the compress runtime; they stay valid until the next
- * compress call or release.  See DESIGN.md for the component layout. */
+ * header fields the host object would have (section offsets/sizes are
+ * payload-relative, `payload` is NULL) with the flags the host can decide
+ * (SVD, outlier).  Whether the error-correction section is present is decided
+ * on the device: the word *d_flags (device memory) has bit 2 set when it is,
+ * and header.section_error_topk describes it for that case.  The component
+ * pointers are device pointers owned by the compress runtime; they stay valid
+ * until the next compress call or release.  For quantised sections d_dense is
+ * NULL and the scales / codes pointers are set; for FP32 sections d_dense is
+ * set. */
 typedef struct {
     bitsqz_llm_array_t header;
     const uint32_t *d_flags;
@@ -179,6 +182,15 @@ BSQ_API int bsq_quant_nf4_codes(const float *d_values, uint64_t n, uint8_t *d_co
 BSQ_API int bsq_quant_e4m3_encode(const float *d_values, uint64_t n, uint8_t *d_codes, void *stream);
 BSQ_API int bsq_quant_e4m3_decode(const uint8_t *d_codes, uint64_t n, float *d_values, void *stream);
 
+/* NF4 code of every float bit pattern in [lo, hi) (hi <= 2^32): 16-bin
+ * histogram and sum over patterns of code * (pattern mod 65521), written to
+ * device memory; pins the device code function against a CPU sweep. */
+BSQ_API int bsq_quant_nf4_code_sweep(uint64_t lo, uint64_t hi, unsigned long long *d_hist16,
+                                     unsigned long long *d_checksum, void *stream);
+/* The 15 exact decision thresholds the device NF4 code function uses for
+ * |v| < 2 (code = number of thresholds <= v). */
+BSQ_API void bsq_nf4_thresholds(float out[15]);
+
 /* Randomised rank-q SVD of a row-major m x n matrix with `niter` power
  * iterations and no oversampling: U (m x q), S (q), V (n x q), row-major,
  * q = max(1, min(q, m, n)).  d_sketch (min(m,n) x q, row-major) may be NULL
@@ -198,6 +210,24 @@ BSQ_API int bsq_reconstruct_lowrank(const float *d_U, const float *d_S, const fl
 /* Fill `n` floats with N(0,1) draws of the built-in sketch generator
  * (counter-based Philox4x32-10 + Box-Muller; deterministic in (seed, index)). */
 BSQ_API int bsq_gaussian_fill(float *d_out, uint64_t n, uint64_t seed, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * 4. Device memory helpers for FFI callers without a GPU framework (no
+ *    reference counterpart; thin wrappers over hipMalloc / hipMemcpy).
+ * ------------------------------------------------------------------------- */
+BSQ_API int bsq_device_count(int *count);
+BSQ_API int bsq_device_malloc(void **ptr, uint64_t bytes);
+BSQ_API int bsq_device_free(void *ptr);
+BSQ_API int bsq_memcpy_h2d(void *dst, const void *src, uint64_t bytes);
+BSQ_API int bsq_memcpy_d2h(void *dst, const void *src, uint64_t bytes);
+BSQ_API int bsq_memcpy_d2d(void *dst, const void *src, uint64_t bytes);
+BSQ_API int bsq_device_memset(void *dst, int value, uint64_t bytes);
+BSQ_API int bsq_stream_synchronize(void *stream);
+/* HIP events on a caller-chosen stream (timing without a GPU framework). */
+BSQ_API int bsq_event_create(void **event);
+BSQ_API int bsq_event_destroy(void *event);
+BSQ_API int bsq_event_record(void *event, void *stream);
+BSQ_API int bsq_event_elapsed_ms(void *start, void *stop, float *ms);
 
 #ifdef __cplusplus
 }

@@ -319,3 +319,23 @@ ORACLE_API int oracle_topk_num_columns(uint16_t cols, float ratio) {
     else if (k == 0 && ratio > 0.0f) k = 1;
     return (int)k;
 }
+
+/* Counts the finite floats with |v| < 2 in the bit-pattern range [lo, hi)
+ * where the threshold rule code = #{c : v >= T[c]} disagrees with the
+ * reference's linear scan (oracle_nf4_code).  Pins the device code
+ * function's shortcut over every input it is used for. */
+ORACLE_API uint64_t oracle_nf4_threshold_mismatches(const float *T, uint64_t lo, uint64_t hi) {
+    uint64_t bad = 0;
+    int64_t p;
+#pragma omp parallel for reduction(+ : bad)
+    for (p = (int64_t)lo; p < (int64_t)hi; ++p) {
+        const uint32_t bits = (uint32_t)p;
+        float v;
+        memcpy(&v, &bits, 4);
+        if (!(fabsf(v) < 2.0f)) continue;
+        unsigned c = 0;
+        for (int i = 0; i < 15; ++i) c += (v >= T[i]) ? 1u : 0u;
+        if (c != oracle_nf4_code(v)) ++bad;
+    }
+    return bad;
+}

@@ -89,6 +89,8 @@ def lib():
         L.oracle_topk_num_columns.restype = ctypes.c_int
         L.oracle_topk_num_columns.argtypes = [ctypes.c_uint16, ctypes.c_float]
         L.oracle_nf4_levels.restype = ctypes.POINTER(ctypes.c_float)
+        L.oracle_nf4_threshold_mismatches.restype = ctypes.c_uint64
+        L.oracle_nf4_threshold_mismatches.argtypes = [P, U64, U64]
         _lib = L
     return _lib
 
@@ -125,6 +127,13 @@ def nf4_code_sweep(lo: int, hi: int):
     cs = np.zeros(1, np.uint64)
     lib().oracle_nf4_code_sweep(lo, hi, _p(hist), _p(cs))
     return hist, int(cs[0])
+
+
+def nf4_threshold_mismatches(thresholds: np.ndarray, lo: int = 0, hi: int = 1 << 32) -> int:
+    """Floats with |v| < 2 in [lo, hi) where code = #{T <= v} differs from the scan."""
+    t = np.ascontiguousarray(thresholds, dtype=np.float32)
+    assert t.size == 15
+    return int(lib().oracle_nf4_threshold_mismatches(_p(t), lo, hi))
 
 
 @dataclass

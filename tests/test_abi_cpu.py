@@ -1,0 +1,166 @@
+"""CPU-side checks of the built library: it loads, exports every symbol the
+headers declare (the nine C++-linkage names of the reference ABI with their
+exact mangling, reference include/bitsqz_llm.hpp:95-141), and its host-only
+entry points (argument validation, packed-size, load) behave as the
+reference's (src/bitsqz_llm.cu:785-804, 887-897, 981-987, 1304-1310,
+1395-1455).  No GPU work is started here."""
+import ctypes as C
+import os
+import re
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+import bitsqz_amd as B
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# Mangled names of the reference's C++-linkage ABI (bitsqz_llm.hpp:95-141)
+# plus topk_compute_num_topk_columns (topk_cuda.cuh, linked by the reference's
+# ABI tests).
+MANGLED = [
+    "_Z30bitsqz_llm_compress_initializettffii21quantization_method_tS_S_27bitsqz_llm_input_location_t",
+    "_Z27bitsqz_llm_compress_releasev",
+    "_Z32bitsqz_llm_decompress_initializettffi21quantization_method_tS_S_",
+    "_Z29bitsqz_llm_decompress_releasev",
+    "_Z19bitsqz_llm_compressPKfPP16bitsqz_llm_arrayP29bitsqz_llm_compress_profile_t",
+    "_Z21bitsqz_llm_decompressPK16bitsqz_llm_arrayPfj",
+    "_Z26bitsqz_llm_get_packed_sizePK16bitsqz_llm_array",
+    "_Z27load_bitsqz_llm_from_bufferPKvm",
+    "_Z15bitsqz_llm_freeP16bitsqz_llm_array",
+    "_Z29topk_compute_num_topk_columnstf",
+]
+
+
+def exported():
+    out = subprocess.run(["nm", "-D", "--defined-only", B.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def c_header_functions():
+    txt = open(os.path.join(ROOT, "include", "bitsqz_llm_c.h")).read()
+    return set(re.findall(r"BSQ_API\s+[\w\s\*]+?\b(bsq_\w+)\s*\(", txt))
+
+
+def test_library_built_and_loads():
+    assert os.path.exists(B.LIB_PATH)
+    assert B.lib().bsq_version().decode().startswith("bitsqz_llm")
+
+
+def test_exports_reference_mangled_abi():
+    syms = exported()
+    missing = [m for m in MANGLED if m not in syms]
+    assert not missing, missing
+
+
+def test_exports_every_c_header_function():
+    syms = exported()
+    decl = c_header_functions()
+    assert len(decl) >= 30
+    missing = sorted(d for d in decl if d not in syms)
+    assert not missing, missing
+
+
+def test_soname_matches_reference_library():
+    out = subprocess.run(["readelf", "-d", B.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    assert "libbitsqz_llm_lib.so.0" in out
+
+
+def test_struct_layout():
+    assert C.sizeof(B.PackedHeader) == 200
+    offs = [getattr(B.PackedHeader, n).offset for n in
+            ("section_u", "section_s", "section_v", "section_direct", "section_outlier_topk",
+             "section_error_topk", "payload")]
+    assert offs == [48, 72, 96, 120, 144, 168, 192]
+    assert C.sizeof(B.Profile) == 56
+
+
+def test_topk_num_columns_matches_reference_rounding():
+    # roundf(cols * ratio), clamped to [1, cols] for ratio > 0 (topk_cuda.cu:53-69)
+    cases = {(4096, 0.005): 20, (4096, 0.01): 41, (14336, 0.002): 29, (14336, 0.005): 72,
+             (11008, 0.005): 55, (11008, 0.01): 110, (6, 0.5): 3, (8, 0.01): 1, (8, 1.0): 8, (8, 0.0): 0,
+             (5, 0.4): 2, (512, 0.03): 15}
+    for (cols, r), k in cases.items():
+        assert B.topk_num_columns(cols, r) == k, (cols, r)
+    with pytest.raises(B.BsqError):
+        B.topk_num_columns(8, 1.5)
+
+
+def test_compress_initialize_rejects_invalid_arguments():
+    bad = [
+        dict(rows=0, cols=8), dict(rows=8, cols=0),
+        dict(rows=8, cols=8, outlier_ratio=-0.1), dict(rows=8, cols=8, error_ratio=1.5),
+        dict(rows=8, cols=8, outlier_ratio=float("nan")),
+        dict(rows=8, cols=8, uv_format=0),  # Q8_0 is rejected (test_quantization.cpp:469-483)
+        dict(rows=8, cols=8, direct_format=5),
+        dict(rows=8, cols=8, input_location=2),
+        dict(rows=8, cols=8, svd_niters=0),
+    ]
+    for kw in bad:
+        rows, cols = kw.pop("rows"), kw.pop("cols")
+        assert B.compress_initialize(rows, cols, **kw) == 1, kw
+    assert B.decompress_initialize(8, 8, uv_format=3) == 1
+    assert B.decompress_initialize(0, 8) == 1
+
+
+def test_calls_before_initialize_fail():
+    B.compress_release()
+    B.decompress_release()
+    out = C.POINTER(B.PackedHeader)()
+    x = np.zeros(64, np.float32)
+    assert B.lib().bsq_compress(x.ctypes.data_as(C.c_void_p), C.byref(out), None) == 1
+    hdr = B.PackedHeader()
+    assert B.lib().bsq_decompress(C.cast(C.pointer(hdr), C.c_void_p), C.c_void_p(16), 64) == 1
+
+
+def _fake_object(sections):
+    """A packed object whose header has the given (offset, size, storage) sections."""
+    hdr = B.PackedHeader()
+    hdr.num_rows, hdr.num_columns, hdr.num_elements = 2, 4, 8
+    names = ["section_u", "section_s", "section_v", "section_direct", "section_outlier_topk",
+             "section_error_topk"]
+    end = 0
+    for name, (off, size, st) in zip(names, sections):
+        s = getattr(hdr, name)
+        s.offset, s.size, s.storage = off, size, st
+        if st:
+            end = max(end, off + size)
+    return bytes(hdr) + bytes(end), end
+
+
+def test_get_packed_size_and_load_validation():
+    L = B.lib()
+    assert L.bsq_get_packed_size(None) == 0
+    buf, end = _fake_object([(0, 0, 0)] * 3 + [(0, 32, 1), (0, 0, 0), (0, 0, 0)])
+    b = C.create_string_buffer(buf, len(buf))
+    p = L.bsq_load_from_buffer(b, len(buf))
+    assert p
+    vp = C.cast(p, C.c_void_p)
+    assert L.bsq_get_packed_size(vp) == 200 + 32
+    # the payload pointer is re-pointed at the copy's own payload
+    assert p.contents.payload == vp.value + 200
+    L.bsq_free(vp)
+    # truncated buffer, short header, bad storage kind, NONE with a size
+    assert not L.bsq_load_from_buffer(b, len(buf) - 1)
+    assert not L.bsq_load_from_buffer(b, 100)
+    for secs in ([(0, 0, 0)] * 3 + [(0, 32, 7), (0, 0, 0), (0, 0, 0)],
+                 [(0, 0, 0)] * 3 + [(0, 0, 1), (0, 0, 0), (0, 0, 0)],
+                 [(0, 4, 0)] + [(0, 0, 0)] * 2 + [(0, 32, 1), (0, 0, 0), (0, 0, 0)]):
+        buf2, _ = _fake_object(secs)
+        b2 = C.create_string_buffer(buf2, max(len(buf2), 200))
+        assert not L.bsq_load_from_buffer(b2, max(len(buf2), 200)), secs
+
+
+def test_device_thresholds_pinned_against_reference_scan():
+    """The device NF4 code function uses code = #{T <= v} for |v| < 2; the
+    thresholds it uses agree with the reference's linear scan on every float
+    with |v| < 2 (2^31 bit patterns, CPU oracle)."""
+    from oracle import oracle as O
+    t = B.nf4_thresholds()
+    assert np.all(np.diff(t) > 0)
+    lv = O.nf4_levels()
+    assert np.all((t > lv[:-1]) & (t < lv[1:]))
+    assert O.nf4_threshold_mismatches(t) == 0

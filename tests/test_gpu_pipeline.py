@@ -1,0 +1,186 @@
+"""The public ABI end to end on the GPU (direct path): packed bytes equal the
+oracle's packed bytes (payload pointer masked), decoded matrices equal the
+oracle's decode bit for bit, and the lifecycle / negative-path contract of the
+reference's ABI tests (tests/bitsqz_llm/test_quantization.cpp:129-461)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import bitsqz_amd as B
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def ref_source(rows, cols, a=0.11, b=0.07):
+    """The reference ABI tests' matrix: sin(a*idx) + cos(b*(r+c)) in float32
+    (test_quantization.cpp:487-492)."""
+    idx = np.arange(rows * cols, dtype=np.int64).reshape(rows, cols)
+    r = np.arange(rows)[:, None]
+    c = np.arange(cols)[None, :]
+    return (np.sin(np.float32(a) * idx.astype(np.float32)) +
+            np.cos(np.float32(b) * (r + c).astype(np.float32))).astype(np.float32)
+
+
+def run_direct(x, outlier=0.0, error=0.0, fmt=B.NF4, loc=B.INPUT_DEVICE):
+    rows, cols = x.shape
+    B.compress_release()
+    B.decompress_release()
+    assert B.compress_initialize(rows, cols, outlier, error, -1, 2, B.QUANT_NONE, B.QUANT_NONE, fmt, loc) == 0
+    assert B.decompress_initialize(rows, cols, outlier, error, -1, B.QUANT_NONE, B.QUANT_NONE, fmt) == 0
+    src = B.DeviceBuffer.from_array(x) if loc == B.INPUT_DEVICE else x
+    data, prof = B.compress(src, profile=True)
+    out = B.decompress(data, rows, cols)
+    return data, out, prof
+
+
+def oracle_direct(x, outlier=0.0, error=0.0, fmt=B.NF4):
+    cfg = O.Config(x.shape[0], x.shape[1], outlier, error, -1, 2, O.QUANT_NONE, O.QUANT_NONE, fmt)
+    p = O.compress(x, cfg)
+    return p.to_bytes(), O.decompress(p)
+
+
+CASES = [
+    # (name, rows, cols, outlier, error, fmt, location)  -- reference test_quantization.cpp:515-519
+    ("quantization_only_nf4", 512, 8192, 0.0, 0.0, B.NF4, B.INPUT_DEVICE),
+    ("quantization_only_nf4_host", 512, 8192, 0.0, 0.0, B.NF4, B.INPUT_HOST),
+    ("quantization_plus_error_nf4", 512, 8192, 0.0, 0.10, B.NF4, B.INPUT_DEVICE),
+    ("outlier_plus_quantization_nf4_dq", 512, 8192, 0.05, 0.0, B.NF4_DQ, B.INPUT_DEVICE),
+    ("outlier_quantization_error_nf4_dq", 512, 8192, 0.05, 0.10, B.NF4_DQ, B.INPUT_DEVICE),
+    ("fp32_direct_outlier", 256, 1000, 0.02, 0.0, B.QUANT_NONE, B.INPUT_HOST),
+    ("fp32_direct_plain", 64, 64, 0.0, 0.3, B.QUANT_NONE, B.INPUT_DEVICE),
+    ("odd_shape_nf4_error", 37, 101, 0.03, 0.07, B.NF4, B.INPUT_DEVICE),
+    ("odd_shape_nf4dq_error", 33, 99, 0.0, 0.5, B.NF4_DQ, B.INPUT_HOST),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_direct_path_bytes_and_decode(case):
+    name, rows, cols, ro, re, fmt, loc = case
+    x = ref_source(rows, cols)
+    data, out, prof = run_direct(x, ro, re, fmt, loc)
+    exp_bytes, exp_out = oracle_direct(x, ro, re, fmt)
+    assert len(data) == len(exp_bytes)
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+    assert prof.other_latency_ms >= 0.0
+
+
+def test_config1_2048x4096_nf4():
+    x = np.random.default_rng(0).standard_normal((2048, 4096)).astype(np.float32)
+    data, out, _ = run_direct(x, 0.0, 0.0, B.NF4)
+    exp_bytes, exp_out = oracle_direct(x, 0.0, 0.0, B.NF4)
+    assert len(data) == 4718840
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+
+
+def test_config2_4096x4096_nf4dq_outliers():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((4096, 4096)).astype(np.float32)
+    cols = np.random.default_rng(1).permutation(4096)[:16]
+    x[:, cols] *= 60.0
+    data, out, _ = run_direct(x, 0.005, 0.0, B.NF4_DQ)
+    exp_bytes, exp_out = oracle_direct(x, 0.005, 0.0, B.NF4_DQ)
+    assert len(data) == 9142528
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+
+
+def test_error_section_absent_when_exact():
+    """A matrix the NF4 codec reproduces exactly has no error section even with
+    error top-k enabled (has_nonzero gate, src/bitsqz_llm.cu:1210-1225)."""
+    x = np.tile(np.array([1.0, -1.0, 0.0, 0.5626170039176941], np.float32), (8, 16))
+    data, out, _ = run_direct(x, 0.0, 0.25, B.NF4)
+    p = O.parse_packed(data)
+    assert not (p.flags & O.FLAG_ERROR) and "error" not in p.sections
+    exp_bytes, exp_out = oracle_direct(x, 0.0, 0.25, B.NF4)
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+
+
+def test_reload_and_negative_paths():
+    """run_case's reload and failure checks (test_quantization.cpp:330-421)."""
+    rows, cols, ro, re, fmt = 128, 512, 0.02, 0.03, B.NF4
+    x = ref_source(rows, cols, 0.09, 0.05)
+    data, out, _ = run_direct(x, ro, re, fmt)
+    dst = B.DeviceBuffer(rows * cols * 4)
+    # reload consistency
+    assert B.decompress_to_device(data, dst, rows * cols) == 0
+    assert np.array_equal(dst.download(np.float32, rows * cols).reshape(rows, cols), out)
+    # destination too small
+    assert B.decompress_to_device(data, dst, rows * cols - 1) == 1
+    # after release
+    B.decompress_release()
+    assert B.decompress_to_device(data, dst, rows * cols) == 1
+    # shape mismatch
+    assert B.decompress_initialize(rows, cols - 1, ro, re, -1, B.QUANT_NONE, B.QUANT_NONE, fmt) == 0
+    assert B.decompress_to_device(data, dst, rows * cols) == 1
+    # no quantisation runtime
+    assert B.decompress_initialize(rows, cols, ro, re, -1, B.QUANT_NONE, B.QUANT_NONE, B.QUANT_NONE) == 0
+    assert B.decompress_to_device(data, dst, rows * cols) == 1
+    # insufficient top-k capacity (smaller_topk_ratio, test_quantization.cpp:43-55)
+    def smaller(ratio):
+        k = B.topk_num_columns(cols, ratio)
+        return 0.0 if k <= 1 else (np.float32(k - 1) - np.float32(0.49)) / np.float32(cols)
+    assert B.decompress_initialize(rows, cols, float(smaller(ro)), float(smaller(re)), -1, B.QUANT_NONE,
+                                   B.QUANT_NONE, fmt) == 0
+    assert B.decompress_to_device(data, dst, rows * cols) == 1
+    # corrupted quant magic
+    bad = bytearray(data)
+    bad[200] ^= 0xFF
+    assert B.decompress_initialize(rows, cols, ro, re, -1, B.QUANT_NONE, B.QUANT_NONE, fmt) == 0
+    assert B.decompress_to_device(bytes(bad), dst, rows * cols) == 1
+    # flags / section mismatch
+    bad = bytearray(data)
+    bad[40] |= 1  # claims SVD
+    assert B.decompress_to_device(bytes(bad), dst, rows * cols) == 1
+    assert B.decompress_to_device(data, dst, rows * cols) == 0
+    B.decompress_release()
+    B.compress_release()
+
+
+def test_lifecycle():
+    """run_lifecycle_checks (test_quantization.cpp:129-230)."""
+    rows, cols = 128, 512
+    x = ref_source(rows, cols, 0.09, 0.05)
+    src = B.DeviceBuffer.from_array(x)
+    dst = B.DeviceBuffer(rows * cols * 4)
+    B.compress_release()
+    B.decompress_release()
+    with pytest.raises(B.BsqError):
+        B.compress(src)
+    args = (rows, cols, 0.02, 0.03)
+    assert B.compress_initialize(*args, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, B.INPUT_DEVICE) == 0
+    assert B.decompress_initialize(*args, -1, B.QUANT_NONE, B.QUANT_NONE, B.NF4) == 0
+    data = B.compress(src)
+    assert B.decompress_to_device(data, dst, rows * cols) == 0
+    B.compress_release()
+    with pytest.raises(B.BsqError):
+        B.compress(src)
+    assert B.decompress_to_device(data, dst, rows * cols) == 0       # survives compressor release
+    assert B.compress_initialize(*args, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, B.INPUT_DEVICE) == 0
+    B.decompress_release()
+    assert B.decompress_to_device(data, dst, rows * cols) == 1
+    data2 = B.compress(src)                                            # survives decompressor release
+    assert O.mask_pointer(data2) == O.mask_pointer(data)
+    # *out must be null on entry
+    out = C.POINTER(B.PackedHeader)(B.PackedHeader())
+    assert B.lib().bsq_compress(src.ptr, C.byref(out), None) == 1
+    B.compress_release()
+
+
+@pytest.mark.parametrize("fmt,ro,re", [(B.NF4, 0.0, 0.0), (B.NF4_DQ, 0.005, 0.01), (B.NF4, 0.02, 0.05)])
+def test_device_resident_matches_abi(fmt, ro, re):
+    rows, cols = 256, 4096
+    x = np.random.default_rng(4).standard_normal((rows, cols)).astype(np.float32)
+    data, out, _ = run_direct(x, ro, re, fmt)
+    src = B.DeviceBuffer.from_array(x)
+    dst = B.DeviceBuffer(rows * cols * 4)
+    packed = B.device_compress(src)
+    B.device_decompress(packed, dst, rows * cols)
+    B.device_synchronize()
+    assert np.array_equal(dst.download(np.float32, rows * cols).reshape(rows, cols), out)
+    B.compress_release()
+    B.decompress_release()
