@@ -1,0 +1,553 @@
+// Small dense FP64 linear algebra for the randomised SVD (k x k, k = rank).
+//
+//   gram      G = X^T X (FP32 X, FP64 products and sums), split over rows
+//   chol_inv  G = L L^T (FP64, shifted retry on breakdown) and L^{-1} as FP32
+//             (CholeskyQR: Q = X L^{-T})
+//   syev      G = U diag(lambda) U^T (FP64): Householder tridiagonalisation,
+//             bisection with Sturm counts, inverse iteration (clusters
+//             re-orthogonalised), back-transformation
+//
+// The reference orthonormalises with Householder QR and finishes with a
+// Jacobi SVD from cuSOLVER (modules/svd_lowrank_cuda/src/svd_lowrank_cuda.cu:
+// 250-282, 390-408); both are replaced here by Gram-based factorisations whose
+// Gram matrices are formed exactly in FP64 from the FP32 factors.
+#include "bsq_internal.hpp"
+
+#include <cfloat>
+
+namespace bsq {
+namespace {
+
+constexpr int kGramTile = 64;
+
+// ---------------------------------------------------------------------------
+// Gram: partial G over a row chunk for one lower 64x64 tile
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gram_partial_kernel(const float *__restrict__ X, int M, int k, int ld,
+                                                            int rows_per_split, double *__restrict__ P) {
+    __shared__ float xi[16][kGramTile + 1];
+    __shared__ float xj[16][kGramTile + 1];
+    // blockIdx.x -> lower tile (ti >= tj)
+    int t = blockIdx.x, ti = 0;
+    while (t > ti) {
+        t -= ti + 1;
+        ++ti;
+    }
+    const int tj = t;
+    const int r0 = blockIdx.y * rows_per_split, r1 = min(M, r0 + rows_per_split);
+    const int ty = threadIdx.x >> 4, tx = threadIdx.x & 15;
+    double acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = 0.0;
+    for (int rb = r0; rb < r1; rb += 16) {
+        for (int e = threadIdx.x; e < 16 * kGramTile; e += 256) {
+            const int rr = e / kGramTile, cc = e % kGramTile;
+            const int r = rb + rr;
+            const int ci = ti * kGramTile + cc, cj = tj * kGramTile + cc;
+            xi[rr][cc] = (r < r1 && ci < k) ? X[static_cast<uint64_t>(r) * ld + ci] : 0.0f;
+            xj[rr][cc] = (r < r1 && cj < k) ? X[static_cast<uint64_t>(r) * ld + cj] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int rr = 0; rr < 16; ++rr) {
+            double a[4], b[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a[q] = static_cast<double>(xi[rr][ty * 4 + q]);
+                b[q] = static_cast<double>(xj[rr][tx * 4 + q]);
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[p][q] = fma(a[p], b[q], acc[p][q]);
+        }
+        __syncthreads();
+    }
+    double *out = P + static_cast<uint64_t>(blockIdx.y) * k * k;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = ti * kGramTile + ty * 4 + p, j = tj * kGramTile + tx * 4 + q;
+            if (i < k && j < k && j <= i) out[static_cast<uint64_t>(i) * k + j] = acc[p][q];
+        }
+}
+
+// G[i][j] = G[j][i] = sum_s P[s][i][j] (lower entries), fixed order.
+__global__ void gram_reduce_kernel(const double *__restrict__ P, int splits, int k, double *__restrict__ G) {
+    const uint64_t kk = static_cast<uint64_t>(k) * k;
+    for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < kk;
+         t += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const int i = static_cast<int>(t / k), j = static_cast<int>(t % k);
+        if (j > i) continue;
+        double s = 0.0;
+        for (int z = 0; z < splits; ++z) s += P[z * kk + t];
+        G[t] = s;
+        G[static_cast<uint64_t>(j) * k + i] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// block helpers (1024 threads)
+// ---------------------------------------------------------------------------
+constexpr int kBig = 1024;
+
+__device__ double block_sum(double v, double *red) {
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double s = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) s += red[w];
+    return s;
+}
+
+__device__ double block_max(double v, double *red) {
+    for (int off = 32; off >= 1; off >>= 1) v = fmax(v, __shfl_xor(v, off));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double s = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) s = fmax(s, red[w]);
+    return s;
+}
+
+// ---------------------------------------------------------------------------
+// Cholesky + triangular inverse, one workgroup, FP64 workspace W (k x k).
+// Output Linv (k x k FP32 row-major, zero above the diagonal) with
+// L^{-1} (G + shift I) L^{-T} = I.  status[0] = number of shifted retries.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBig) void chol_inv_kernel(const double *__restrict__ G, int k,
+                                                         double *__restrict__ W, float *__restrict__ Linv,
+                                                         int *__restrict__ status) {
+    extern __shared__ double col[];  // k doubles
+    __shared__ double red[kBig / 64];
+    __shared__ int broke;
+    const int tid = threadIdx.x;
+    double dmax = 0.0;
+    for (int i = tid; i < k; i += kBig) dmax = fmax(dmax, fabs(G[static_cast<uint64_t>(i) * k + i]));
+    dmax = block_max(dmax, red);
+    double shift = 0.0;
+    int attempt = 0;
+    for (;; ++attempt) {
+        // W = lower(G) + shift I
+        for (uint64_t t = tid; t < static_cast<uint64_t>(k) * k; t += kBig) {
+            const int i = static_cast<int>(t / k), j = static_cast<int>(t % k);
+            W[t] = (j <= i) ? G[t] + (i == j ? shift : 0.0) : 0.0;
+        }
+        if (tid == 0) broke = 0;
+        __syncthreads();
+        const double tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
+        for (int j = 0; j < k; ++j) {
+            const double d = W[static_cast<uint64_t>(j) * k + j];
+            if (!(d > tiny)) {  // not positive definite at working precision (also NaN)
+                if (tid == 0) broke = 1;
+                __syncthreads();
+                break;
+            }
+            const double dj = sqrt(d);
+            for (int i = j + 1 + tid; i < k; i += kBig) {
+                const double v = W[static_cast<uint64_t>(i) * k + j] / dj;
+                W[static_cast<uint64_t>(i) * k + j] = v;
+                col[i] = v;
+            }
+            __syncthreads();
+            if (tid == 0) W[static_cast<uint64_t>(j) * k + j] = dj;
+            const int n = k - j - 1;  // trailing lower triangle, rows/cols j+1..k-1
+            for (int i2 = tid >> 5; i2 < n; i2 += kBig / 32) {
+                const int i = j + 1 + i2;
+                const double li = col[i];
+                double *row = W + static_cast<uint64_t>(i) * k;
+                for (int c2 = tid & 31; c2 <= i2; c2 += 32) {
+                    const int c = j + 1 + c2;
+                    row[c] -= li * col[c];
+                }
+            }
+            __syncthreads();
+        }
+        if (!broke) break;
+        if (attempt >= 6 || dmax == 0.0) {
+            // zero or hopeless matrix: L = I
+            for (uint64_t t = tid; t < static_cast<uint64_t>(k) * k; t += kBig) {
+                const int i = static_cast<int>(t / k), j = static_cast<int>(t % k);
+                W[t] = (i == j) ? 1.0 : 0.0;
+            }
+            __syncthreads();
+            break;
+        }
+        shift = (shift == 0.0) ? dmax * 1e-12 * static_cast<double>(k) : shift * 100.0;
+        __syncthreads();
+    }
+    // in-place inverse of the lower-triangular W (column j from the bottom up):
+    // Linv[j][j] = 1 / L[j][j];  Linv[j+1:, j] = -Linv[j][j] * Linv[j+1:, j+1:] L[j+1:, j]
+    for (int j = k - 1; j >= 0; --j) {
+        const double ljj = 1.0 / W[static_cast<uint64_t>(j) * k + j];  // read before thread 0 overwrites it
+        for (int i = j + 1 + tid; i < k; i += kBig) col[i] = W[static_cast<uint64_t>(i) * k + j];
+        __syncthreads();
+        for (int i = j + 1 + tid; i < k; i += kBig) {
+            const double *row = W + static_cast<uint64_t>(i) * k;
+            double s = 0.0;
+            for (int m = j + 1; m <= i; ++m) s = fma(row[m], col[m], s);
+            W[static_cast<uint64_t>(i) * k + j] = -ljj * s;
+        }
+        if (tid == 0) W[static_cast<uint64_t>(j) * k + j] = ljj;
+        __syncthreads();
+    }
+    for (uint64_t t = tid; t < static_cast<uint64_t>(k) * k; t += kBig) {
+        const int i = static_cast<int>(t / k), j = static_cast<int>(t % k);
+        Linv[t] = (j <= i) ? static_cast<float>(W[t]) : 0.0f;
+    }
+    if (tid == 0 && status) status[0] = attempt;
+}
+
+// ---------------------------------------------------------------------------
+// Householder tridiagonalisation of the symmetric W (full storage, in place):
+// d[0..k), e[0..k-1), reflector j stored in W[j+1.., j] (first entry 1),
+// tau[j].  One workgroup.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBig) void sytrd_kernel(double *__restrict__ W, int k, double *__restrict__ d,
+                                                      double *__restrict__ e, double *__restrict__ tau) {
+    extern __shared__ double sm[];  // v[k], p[k]
+    double *v = sm, *p = sm + k;
+    __shared__ double red[kBig / 64];
+    const int tid = threadIdx.x;
+    for (int j = 0; j + 2 < k; ++j) {
+        const int n = k - j - 1;  // length of the reflector, rows j+1..k-1
+        double sig = 0.0;
+        for (int i = 1 + tid; i < n; i += kBig) {
+            const double x = W[static_cast<uint64_t>(j + 1 + i) * k + j];
+            sig = fma(x, x, sig);
+        }
+        sig = block_sum(sig, red);
+        const double alpha = W[static_cast<uint64_t>(j + 1) * k + j];
+        double t = 0.0, beta = alpha;
+        if (sig > 0.0) {
+            const double nrm = sqrt(fma(alpha, alpha, sig));
+            beta = (alpha >= 0.0) ? -nrm : nrm;
+            t = (beta - alpha) / beta;
+            const double scal = 1.0 / (alpha - beta);
+            for (int i = tid; i < n; i += kBig)
+                v[i] = (i == 0) ? 1.0 : W[static_cast<uint64_t>(j + 1 + i) * k + j] * scal;
+        } else {
+            for (int i = tid; i < n; i += kBig) v[i] = (i == 0) ? 1.0 : 0.0;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            d[j] = W[static_cast<uint64_t>(j) * k + j];
+            e[j] = beta;
+            tau[j] = t;
+        }
+        // store the reflector in column j below the diagonal
+        for (int i = tid; i < n; i += kBig) W[static_cast<uint64_t>(j + 1 + i) * k + j] = v[i];
+        if (t != 0.0) {
+            // p = t * A' v  (A' = trailing block, full symmetric storage)
+            for (int i = tid; i < n; i += kBig) {
+                double s = 0.0;
+                for (int c = 0; c < n; ++c) s = fma(W[static_cast<uint64_t>(j + 1 + c) * k + (j + 1 + i)], v[c], s);
+                p[i] = t * s;
+            }
+            __syncthreads();
+            double pv = 0.0;
+            for (int i = tid; i < n; i += kBig) pv = fma(p[i], v[i], pv);
+            pv = block_sum(pv, red);
+            const double half = 0.5 * t * pv;
+            for (int i = tid; i < n; i += kBig) p[i] -= half * v[i];  // p <- w
+            __syncthreads();
+            // A' -= v w^T + w v^T
+            const uint64_t nn = static_cast<uint64_t>(n) * n;
+            for (uint64_t q = tid; q < nn; q += kBig) {
+                const int r = static_cast<int>(q / n), c = static_cast<int>(q % n);
+                double *a = W + static_cast<uint64_t>(j + 1 + r) * k + (j + 1 + c);
+                *a -= v[r] * p[c] + p[r] * v[c];
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        if (k >= 2) {
+            d[k - 2] = W[static_cast<uint64_t>(k - 2) * k + (k - 2)];
+            e[k - 2] = W[static_cast<uint64_t>(k - 1) * k + (k - 2)];
+            tau[k - 2] = 0.0;
+        }
+        d[k - 1] = W[static_cast<uint64_t>(k - 1) * k + (k - 1)];
+        if (k >= 1) tau[k - 1] = 0.0;
+    }
+}
+
+// Number of eigenvalues of the tridiagonal (d, e) strictly below x.
+__device__ int sturm_count(const double *d, const double *e2, int k, double x, double pivmin) {
+    int cnt = 0;
+    double q = d[0] - x;
+    if (fabs(q) < pivmin) q = -pivmin;
+    cnt += (q < 0.0);
+    for (int i = 1; i < k; ++i) {
+        q = (d[i] - x) - e2[i - 1] / q;
+        if (fabs(q) < pivmin) q = -pivmin;
+        cnt += (q < 0.0);
+    }
+    return cnt;
+}
+
+// lambda[t] = t-th largest eigenvalue (bisection to full precision).
+__global__ void bisect_kernel(const double *__restrict__ d, const double *__restrict__ e, int k,
+                              double *__restrict__ lambda, double *__restrict__ e2buf) {
+    extern __shared__ double sm[];  // d[k], e2[k]
+    double *sd = sm, *se2 = sm + k;
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+        sd[i] = d[i];
+        se2[i] = (i + 1 < k) ? e[i] * e[i] : 0.0;
+    }
+    __syncthreads();
+    // Gershgorin bounds and pivmin (computed redundantly per workgroup)
+    double lo = 1e300, hi = -1e300, emax = 0.0;
+    for (int i = 0; i < k; ++i) {
+        const double r = (i > 0 ? sqrt(se2[i - 1]) : 0.0) + (i + 1 < k ? sqrt(se2[i]) : 0.0);
+        lo = fmin(lo, sd[i] - r);
+        hi = fmax(hi, sd[i] + r);
+        if (i + 1 < k) emax = fmax(emax, se2[i]);
+    }
+    const double tnorm = fmax(fabs(lo), fabs(hi));
+    const double pivmin = fmax(DBL_MIN, DBL_MIN * emax) * 4.0 + tnorm * 1e-300;
+    lo -= 2.0 * tnorm * DBL_EPSILON * k + pivmin;
+    hi += 2.0 * tnorm * DBL_EPSILON * k + pivmin;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= k) return;
+    const int target = k - 1 - t;  // ascending index
+    double a = lo, b = hi;
+    for (int it = 0; it < 200; ++it) {
+        const double mid = 0.5 * (a + b);
+        if (mid <= a || mid >= b) break;
+        if (b - a <= 2.0 * DBL_EPSILON * fmax(fabs(a), fabs(b)) + pivmin) break;
+        if (sturm_count(sd, se2, k, mid, pivmin) > target) b = mid;
+        else a = mid;
+    }
+    lambda[t] = 0.5 * (a + b);
+    if (t == 0 && e2buf) e2buf[0] = tnorm;
+}
+
+// Solves (T - lam I) x = b in place on b with Gaussian elimination with
+// partial pivoting on the tridiagonal (LAPACK dlagtf / dlagts in spirit);
+// zero pivots are replaced by `tiny`.  Scratch arrays of length k.
+__device__ void trid_solve(const double *d, const double *e, int k, double lam, double tiny, double *b,
+                           double *u0, double *u1, double *u2, double *ml, int *piv) {
+    // factor rows: U has diag u0, super u1, super-super u2
+    double dcur = d[0] - lam, ecur = (k > 1) ? e[0] : 0.0;
+    for (int i = 0; i < k - 1; ++i) {
+        const double sub = e[i];                 // T[i+1][i]
+        const double dn = d[i + 1] - lam;        // T[i+1][i+1]
+        const double en = (i + 2 < k) ? e[i + 1] : 0.0;  // T[i+1][i+2]
+        if (fabs(dcur) >= fabs(sub)) {
+            piv[i] = 0;
+            double p = dcur;
+            if (p == 0.0) p = tiny;
+            const double m = sub / p;
+            ml[i] = m;
+            u0[i] = p;
+            u1[i] = ecur;
+            u2[i] = 0.0;
+            dcur = dn - m * ecur;
+            ecur = en;
+        } else {
+            piv[i] = 1;
+            const double m = dcur / sub;
+            ml[i] = m;
+            u0[i] = sub;
+            u1[i] = dn;
+            u2[i] = en;
+            dcur = ecur - m * dn;
+            ecur = -m * en;
+        }
+    }
+    u0[k - 1] = (dcur == 0.0) ? tiny : dcur;
+    // forward: apply L^{-1} P
+    for (int i = 0; i < k - 1; ++i) {
+        if (piv[i]) {
+            const double t = b[i];
+            b[i] = b[i + 1];
+            b[i + 1] = t;
+        }
+        b[i + 1] -= ml[i] * b[i];
+    }
+    // backward: U x = b
+    for (int i = k - 1; i >= 0; --i) {
+        double s = b[i];
+        if (i + 1 < k) s -= u1[i] * b[i + 1];
+        if (i + 2 < k) s -= u2[i] * b[i + 2];
+        double p = u0[i];
+        if (fabs(p) < tiny) p = (p < 0.0) ? -tiny : tiny;
+        b[i] = s / p;
+    }
+}
+
+__device__ __forceinline__ double start_entry(int t, int i) {
+    // deterministic pseudo-random start vector
+    uint32_t h = static_cast<uint32_t>(t) * 0x9E3779B9u ^ (static_cast<uint32_t>(i) + 0x7F4A7C15u) * 0x85EBCA6Bu;
+    h ^= h >> 13;
+    h *= 0xC2B2AE35u;
+    h ^= h >> 16;
+    return 0.5 + static_cast<double>(h & 0xFFFF) / 65536.0;
+}
+
+// Inverse iteration, one thread per eigenvalue: Z[t][0..k) = eigenvector of
+// the tridiagonal for lambda[t].  scratch: 5 k doubles + k ints per thread.
+__global__ void invit_kernel(const double *__restrict__ d, const double *__restrict__ e, int k,
+                             const double *__restrict__ lambda, const double *__restrict__ tnorm_p,
+                             double *__restrict__ Z, double *__restrict__ scratch, int *__restrict__ iscratch) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= k) return;
+    const double tnorm = fmax(tnorm_p[0], DBL_MIN);
+    const double tiny = tnorm * DBL_EPSILON;
+    double *b = Z + static_cast<uint64_t>(t) * k;
+    double *sc = scratch + static_cast<uint64_t>(t) * 4 * k;
+    int *piv = iscratch + static_cast<uint64_t>(t) * k;
+    const double lam = lambda[t];
+    for (int i = 0; i < k; ++i) b[i] = start_entry(t, i);
+    for (int it = 0; it < 3; ++it) {
+        trid_solve(d, e, k, lam, tiny, b, sc, sc + k, sc + 2 * k, sc + 3 * k, piv);
+        double nrm = 0.0;
+        for (int i = 0; i < k; ++i) nrm = fma(b[i], b[i], nrm);
+        nrm = sqrt(nrm);
+        const double inv = nrm > 0.0 ? 1.0 / nrm : 0.0;
+        for (int i = 0; i < k; ++i) b[i] *= inv;
+    }
+}
+
+// Re-runs inverse iteration for eigenvalue clusters (gap below
+// 1e-9 * ||T||), one workgroup per cluster, orthogonalising each member
+// against the earlier members after every solve.
+__global__ void cluster_kernel(const double *__restrict__ d, const double *__restrict__ e, int k,
+                               const double *__restrict__ lambda, const double *__restrict__ tnorm_p,
+                               double *__restrict__ Z, double *__restrict__ scratch, int *__restrict__ iscratch) {
+    __shared__ double red[16];
+    __shared__ double bcast;
+    const int c0 = blockIdx.x;
+    const double tnorm = fmax(tnorm_p[0], DBL_MIN);
+    const double tol = 1e-9 * tnorm;
+    auto close = [&](int a) { return fabs(lambda[a] - lambda[a + 1]) <= tol; };
+    if (c0 + 1 >= k || !close(c0)) return;
+    if (c0 > 0 && close(c0 - 1)) return;  // not the first member
+    int c1 = c0 + 1;
+    while (c1 + 1 < k && close(c1)) ++c1;
+    const double tiny = tnorm * DBL_EPSILON;
+    double *sc = scratch + static_cast<uint64_t>(c0) * 4 * k;
+    int *piv = iscratch + static_cast<uint64_t>(c0) * k;
+    for (int t = c0; t <= c1; ++t) {
+        double *b = Z + static_cast<uint64_t>(t) * k;
+        for (int i = threadIdx.x; i < k; i += blockDim.x) b[i] = start_entry(t + 977, i) - 0.5;
+        __syncthreads();
+        for (int it = 0; it < 3; ++it) {
+            if (threadIdx.x == 0) trid_solve(d, e, k, lambda[t], tiny, b, sc, sc + k, sc + 2 * k, sc + 3 * k, piv);
+            __syncthreads();
+            for (int pass = 0; pass < 2; ++pass) {
+                for (int s = c0; s < t; ++s) {
+                    const double *z = Z + static_cast<uint64_t>(s) * k;
+                    double dot = 0.0;
+                    for (int i = threadIdx.x; i < k; i += blockDim.x) dot = fma(z[i], b[i], dot);
+                    dot = block_sum(dot, red);
+                    for (int i = threadIdx.x; i < k; i += blockDim.x) b[i] -= dot * z[i];
+                    __syncthreads();
+                }
+            }
+            double nrm = 0.0;
+            for (int i = threadIdx.x; i < k; i += blockDim.x) nrm = fma(b[i], b[i], nrm);
+            nrm = block_sum(nrm, red);
+            if (threadIdx.x == 0) bcast = nrm > 0.0 ? 1.0 / sqrt(nrm) : 0.0;
+            __syncthreads();
+            const double inv = bcast;
+            for (int i = threadIdx.x; i < k; i += blockDim.x) b[i] *= inv;
+            __syncthreads();
+        }
+    }
+}
+
+// Back-transformation: u_t = H_0 H_1 ... H_{k-3} z_t, one wave per
+// eigenvector; writes Uh[i][t] (FP32, row-major k x k).
+__global__ void backtransform_kernel(const double *__restrict__ W, const double *__restrict__ tau, int k,
+                                     double *__restrict__ Z, float *__restrict__ Uh) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (t >= k) return;
+    double *z = Z + static_cast<uint64_t>(t) * k;
+    for (int j = k - 3; j >= 0; --j) {
+        const double tj = tau[j];
+        if (tj == 0.0) continue;
+        // v has v[0] = 1 at row j+1, then W[j+2.., j]
+        double s = 0.0;
+        for (int i = j + 1 + lane; i < k; i += 64) {
+            const double vi = (i == j + 1) ? 1.0 : W[static_cast<uint64_t>(i) * k + j];
+            s = fma(vi, z[i], s);
+        }
+        for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+        s *= tj;
+        for (int i = j + 1 + lane; i < k; i += 64) {
+            const double vi = (i == j + 1) ? 1.0 : W[static_cast<uint64_t>(i) * k + j];
+            z[i] -= s * vi;
+        }
+    }
+    for (int i = lane; i < k; i += 64) Uh[static_cast<uint64_t>(i) * k + t] = static_cast<float>(z[i]);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+uint64_t gram_workspace_bytes(int M, int k) {
+    const int nt = static_cast<int>(ceil_div(k, kGramTile));
+    const int tiles = nt * (nt + 1) / 2;
+    int splits = static_cast<int>(ceil_div(static_cast<uint64_t>(cu_count()) * 2, tiles));
+    splits = std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 256))));
+    return static_cast<uint64_t>(splits) * k * k * sizeof(double);
+}
+
+void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream) {
+    const int nt = static_cast<int>(ceil_div(k, kGramTile));
+    const int tiles = nt * (nt + 1) / 2;
+    int splits = static_cast<int>(ceil_div(static_cast<uint64_t>(cu_count()) * 2, tiles));
+    splits = std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 256))));
+    const int rows_per = static_cast<int>(ceil_div(ceil_div(M, splits), 16) * 16);
+    splits = static_cast<int>(ceil_div(M, rows_per));
+    gram_partial_kernel<<<dim3(tiles, splits), 256, 0, stream>>>(X, M, k, ld, rows_per, workspace);
+    BSQ_HIP(hipGetLastError());
+    const uint64_t kk = static_cast<uint64_t>(k) * k;
+    const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(ceil_div(kk, 256), 1024));
+    gram_reduce_kernel<<<grid, 256, 0, stream>>>(workspace, splits, k, G);
+    BSQ_HIP(hipGetLastError());
+}
+
+void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(k) * sizeof(double);
+    BSQ_REQUIRE(lds <= 64 * 1024, "chol_inv: rank too large");
+    chol_inv_kernel<<<1, kBig, lds, stream>>>(G, k, W, Linv, status);
+    BSQ_HIP(hipGetLastError());
+}
+
+// Eigen-decomposition of the symmetric G (k x k FP64): lambda descending,
+// Uh[i][t] = component i of eigenvector t (FP32).  `W` k*k doubles, `Z`
+// k*k doubles, `small` >= 4k + 8 doubles, `scratch` 4*k*k doubles,
+// `iscratch` k*k ints.
+void launch_syev(const double *G, int k, double *W, double *Z, double *small, double *scratch, int *iscratch,
+                 double *lambda, float *Uh, hipStream_t stream) {
+    BSQ_REQUIRE(k >= 1 && static_cast<size_t>(2 * k) * sizeof(double) <= 64 * 1024, "syev: rank too large");
+    double *d = small, *e = small + k, *tau = small + 2 * k, *tn = small + 3 * k;
+    BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));
+    sytrd_kernel<<<1, kBig, 2 * k * sizeof(double), stream>>>(W, k, d, e, tau);
+    BSQ_HIP(hipGetLastError());
+    const int bthreads = 256;
+    bisect_kernel<<<static_cast<unsigned>(ceil_div(k, bthreads)), bthreads, 2 * k * sizeof(double), stream>>>(
+        d, e, k, lambda, tn);
+    BSQ_HIP(hipGetLastError());
+    invit_kernel<<<static_cast<unsigned>(ceil_div(k, 64)), 64, 0, stream>>>(d, e, k, lambda, tn, Z, scratch,
+                                                                           iscratch);
+    BSQ_HIP(hipGetLastError());
+    cluster_kernel<<<k, 256, 0, stream>>>(d, e, k, lambda, tn, Z, scratch, iscratch);
+    BSQ_HIP(hipGetLastError());
+    backtransform_kernel<<<static_cast<unsigned>(ceil_div(k, 4)), 256, 0, stream>>>(W, tau, k, Z, Uh);
+    BSQ_HIP(hipGetLastError());
+}
+
+}  // namespace bsq

@@ -225,8 +225,9 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
         }
         if (valid) {
             uint32_t c[8];
+            const uint64_t e0 = chunk * 8;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) c[i] = nf4_code(v[i] * inv);
+            for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code(v[i] * inv) : 0u;  // odd tail: low nibble 0
             store_codes(codes, n, chunk, vec_ok, c);
         }
     }

@@ -1,7 +1,37 @@
-// Randomised low-rank SVD (placeholder plan) + reconstruction + sketch generator.
+// Randomised rank-q SVD (range finder with power iterations), the low-rank
+// reconstruction and the Gaussian sketch generator.
+//
+// Algorithm (reference modules/svd_lowrank_cuda/src/svd_lowrank_cuda.cu:
+// 129-137, 284-426, 478-524): with A_w = A (m >= n) or A^T (m < n), of size
+// M_w x N_w, and k = max(1, min(q, m, n)) (no oversampling):
+//     X = A_w R; Q = orth(X)
+//     repeat niter: Q' = orth(A_w^T Q); Q = orth(A_w Q')
+//     B = Q^T A_w = U_hat S V_hat^T;  U_w = Q U_hat
+//     outputs (row-major): U = U_w, V = V_hat, or swapped when m < n.
+// Design on MI355X: the big matrix is read in place (row-major, as op(A) or
+// op(A)^T inside the MFMA GEMM, no transposed copy); orth() is CholeskyQR
+// with the Gram matrix formed in FP64 (twice for the final basis); the SVD of
+// B is taken from the FP64 eigen-decomposition of B B^T = Y^T Y with
+// Y = A_w^T Q, so that U_hat comes from a k x k problem and
+// V_hat = Y U_hat / S by one more GEMM.  Signs are normalised so that the
+// largest-magnitude entry of every column of U is positive.
 #include "bsq_internal.hpp"
 
+#include <algorithm>
+
 namespace bsq {
+
+// launchers from gemm.hip / linalg.hip
+uint64_t gemm_workspace_bytes(int M, int N, int K);
+void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda, const float *B, int ldb, float *C,
+                 int ldc, const float *a_colscale, const float *minuend, float *workspace, uint64_t workspace_bytes,
+                 hipStream_t stream);
+uint64_t gram_workspace_bytes(int M, int k);
+void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream);
+void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream);
+void launch_syev(const double *G, int k, double *W, double *Z, double *small, double *scratch, int *iscratch,
+                 double *lambda, float *Uh, hipStream_t stream);
+
 namespace {
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
@@ -42,62 +72,233 @@ __global__ void gaussian_fill_kernel(float *__restrict__ out, uint64_t n, uint64
     }
 }
 
-// out[i, j] = (minuend[i, j] -) sum_k (U[i, k] * S[k]) * V[j, k]
-constexpr int kT = 16;
-__global__ void reconstruct_simple_kernel(const float *__restrict__ U, const float *__restrict__ S,
-                                          const float *__restrict__ V, int m, int n, int k,
-                                          const float *__restrict__ minuend, float *__restrict__ out) {
-    __shared__ float us[kT][kT + 1];
-    __shared__ float vs[kT][kT + 1];
-    const int i = blockIdx.y * kT + threadIdx.y, j = blockIdx.x * kT + threadIdx.x;
-    float acc = 0.0f;
-    for (int k0 = 0; k0 < k; k0 += kT) {
-        const int ku = k0 + threadIdx.x;
-        const int iu = blockIdx.y * kT + threadIdx.y;
-        us[threadIdx.y][threadIdx.x] = (iu < m && ku < k) ? U[static_cast<uint64_t>(iu) * k + ku] * S[ku] : 0.0f;
-        const int jv = blockIdx.x * kT + threadIdx.y;
-        vs[threadIdx.y][threadIdx.x] = (jv < n && ku < k) ? V[static_cast<uint64_t>(jv) * k + ku] : 0.0f;
-        __syncthreads();
-#pragma unroll
-        for (int t = 0; t < kT; ++t) acc = fmaf(us[threadIdx.y][t], vs[threadIdx.x][t], acc);
-        __syncthreads();
+// S[t] = sqrt(max(lambda[t], 0))
+__global__ void sqrt_eig_kernel(const double *__restrict__ lambda, int k, float *__restrict__ S) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < k) S[t] = static_cast<float>(sqrt(fmax(lambda[t], 0.0)));
+}
+
+// Column t of V (rows x k, row-major) divided by its 2-norm (FP64 sum).
+__global__ void col_normalize_kernel(float *__restrict__ V, int rows, int k) {
+    __shared__ double red[4];
+    const int t = blockIdx.x;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < rows; i += blockDim.x) {
+        const double v = V[static_cast<uint64_t>(i) * k + t];
+        s = fma(v, v, s);
     }
-    if (i < m && j < n) {
-        const uint64_t e = static_cast<uint64_t>(i) * n + j;
-        out[e] = minuend ? minuend[e] - acc : acc;
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    if (!(tot > 0.0)) return;
+    const float inv = static_cast<float>(1.0 / sqrt(tot));
+    for (int i = threadIdx.x; i < rows; i += blockDim.x) V[static_cast<uint64_t>(i) * k + t] *= inv;
+}
+
+// Flip column t of U and V when the first largest-|.| entry of U[:, t] is
+// negative.
+__global__ void sign_fix_kernel(float *__restrict__ U, int m, float *__restrict__ V, int n, int k) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const int t = blockIdx.x;
+    float best = -1.0f;
+    int bidx = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < m; i += blockDim.x) {
+        const float a = fabsf(U[static_cast<uint64_t>(i) * k + t]);
+        if (a > best) {
+            best = a;
+            bidx = i;
+        }
     }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ob = __shfl_xor(best, off);
+        const int oi = __shfl_xor(bidx, off);
+        if (ob > best || (ob == best && oi < bidx)) {
+            best = ob;
+            bidx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = best;
+        bi[threadIdx.x >> 6] = bidx;
+    }
+    __syncthreads();
+    float b = bv[0];
+    int idx = bi[0];
+    for (int w = 1; w < 4; ++w)
+        if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
+            b = bv[w];
+            idx = bi[w];
+        }
+    if (idx >= m || !(U[static_cast<uint64_t>(idx) * k + t] < 0.0f)) return;
+    for (int i = threadIdx.x; i < m; i += blockDim.x) U[static_cast<uint64_t>(i) * k + t] *= -1.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) V[static_cast<uint64_t>(i) * k + t] *= -1.0f;
+}
+
+template <typename T>
+T *alloc(uint64_t count) {
+    if (count == 0) return nullptr;
+    void *p = nullptr;
+    BSQ_HIP(hipMalloc(&p, count * sizeof(T)));
+    return static_cast<T *>(p);
+}
+
+template <typename T>
+void release(T *&p) noexcept {
+    if (p) (void)hipFree(p);
+    p = nullptr;
 }
 
 }  // namespace
 
 struct SvdPlan {
-    int m = 0, n = 0, q = 0, niter = 0;
+    int m = 0, n = 0, k = 0, niter = 0;
+    bool transposed = false;
+    int Mw = 0, Nw = 0;
+    float *R = nullptr, *X = nullptr, *X2 = nullptr, *Y = nullptr, *Y2 = nullptr;
+    float *Linv = nullptr, *Uh = nullptr;
+    double *G = nullptr, *W = nullptr, *Z = nullptr, *small = nullptr, *scratch = nullptr, *lambda = nullptr;
+    int *iscratch = nullptr, *status = nullptr;
+    double *gram_ws = nullptr;
+    float *gemm_ws = nullptr;
+    uint64_t gemm_ws_bytes = 0;
+
+    ~SvdPlan() {
+        release(R);
+        release(X);
+        release(X2);
+        release(Y);
+        release(Y2);
+        release(Linv);
+        release(Uh);
+        release(G);
+        release(W);
+        release(Z);
+        release(small);
+        release(scratch);
+        release(lambda);
+        release(iscratch);
+        release(status);
+        release(gram_ws);
+        release(gemm_ws);
+    }
 };
 
 SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
     BSQ_REQUIRE(m > 0 && n > 0 && q > 0 && niter >= 0, "svd: bad arguments");
     auto *p = new SvdPlan;
-    p->m = m;
-    p->n = n;
-    p->q = std::max(1, std::min(q, std::min(m, n)));
-    p->niter = niter;
+    try {
+        p->m = m;
+        p->n = n;
+        p->k = std::max(1, std::min(q, std::min(m, n)));
+        p->niter = niter;
+        p->transposed = m < n;
+        p->Mw = p->transposed ? n : m;
+        p->Nw = p->transposed ? m : n;
+        const uint64_t k = p->k;
+        BSQ_REQUIRE(k <= 4096, "svd: rank above the supported maximum (4096)");
+        p->R = alloc<float>(p->Nw * k);
+        p->X = alloc<float>(p->Mw * k);
+        p->X2 = alloc<float>(p->Mw * k);
+        p->Y = alloc<float>(p->Nw * k);
+        p->Y2 = alloc<float>(p->Nw * k);
+        p->Linv = alloc<float>(k * k);
+        p->Uh = alloc<float>(k * k);
+        p->G = alloc<double>(k * k);
+        p->W = alloc<double>(k * k);
+        p->Z = alloc<double>(k * k);
+        p->small = alloc<double>(4 * k + 8);
+        p->scratch = alloc<double>(4 * k * k);
+        p->lambda = alloc<double>(k);
+        p->iscratch = alloc<int>(k * k);
+        p->status = alloc<int>(4);
+        const uint64_t gw = std::max(gram_workspace_bytes(p->Mw, p->k), gram_workspace_bytes(p->Nw, p->k));
+        p->gram_ws = alloc<double>(gw / sizeof(double) + 1);
+        uint64_t ws = 0;
+        ws = std::max(ws, gemm_workspace_bytes(p->Mw, p->k, p->Nw));
+        ws = std::max(ws, gemm_workspace_bytes(p->Nw, p->k, p->Mw));
+        p->gemm_ws_bytes = ws;
+        p->gemm_ws = ws ? alloc<float>(ws / sizeof(float)) : nullptr;
+    } catch (...) {
+        delete p;
+        throw;
+    }
     return p;
 }
 
 void svd_plan_destroy(SvdPlan *plan) noexcept { delete plan; }
 
-int svd_plan_rank(const SvdPlan *plan) { return plan ? plan->q : 0; }
+int svd_plan_rank(const SvdPlan *plan) { return plan ? plan->k : 0; }
 
-void svd_run(SvdPlan *, const float *, const float *, uint64_t, float *, float *, float *, hipStream_t) {
-    fail("svd_lowrank: not implemented yet");
+void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, float *U, float *S, float *V,
+             hipStream_t st) {
+    BSQ_REQUIRE(p && A && U && S && V, "svd: null argument");
+    const int m = p->m, n = p->n, k = p->k, Mw = p->Mw, Nw = p->Nw;
+    const float *R = sketch;
+    if (!R) {
+        launch_gaussian_fill(p->R, static_cast<uint64_t>(Nw) * k, seed, st);
+        R = p->R;
+    }
+    // X (Mw x k) = A_w * B (B is Nw x k)
+    auto aw_times = [&](const float *Bm, float *out) {
+        if (!p->transposed) launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
+                                        p->gemm_ws_bytes, st);
+        else launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws, p->gemm_ws_bytes,
+                         st);
+    };
+    // Y (Nw x k) = A_w^T * B (B is Mw x k)
+    auto awt_times = [&](const float *Bm, float *out) {
+        if (!p->transposed) launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
+                                        p->gemm_ws_bytes, st);
+        else launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws, p->gemm_ws_bytes,
+                         st);
+    };
+    // one CholeskyQR pass: out = in * L^{-T}, G = in^T in = L L^T
+    auto orth = [&](const float *in, float *out, int rows) {
+        launch_gram(in, rows, k, k, p->G, p->gram_ws, st);
+        launch_chol_inv(p->G, k, p->W, p->Linv, p->status, st);
+        launch_gemm(false, true, rows, k, k, in, k, p->Linv, k, out, k, nullptr, nullptr, p->gemm_ws,
+                    p->gemm_ws_bytes, st);
+    };
+    float *Xa = p->X, *Xb = p->X2, *Ya = p->Y, *Yb = p->Y2;
+    aw_times(R, Xa);
+    orth(Xa, Xb, Mw);
+    std::swap(Xa, Xb);
+    for (int it = 0; it < p->niter; ++it) {
+        awt_times(Xa, Ya);
+        orth(Ya, Yb, Nw);
+        std::swap(Ya, Yb);
+        aw_times(Ya, Xa);
+        orth(Xa, Xb, Mw);
+        std::swap(Xa, Xb);
+    }
+    // second CholeskyQR pass on the final basis (CholeskyQR2)
+    orth(Xa, Xb, Mw);
+    std::swap(Xa, Xb);
+    // Y = A_w^T Q = B^T;  B B^T = Y^T Y = U_hat diag(S^2) U_hat^T
+    awt_times(Xa, Ya);
+    launch_gram(Ya, Nw, k, k, p->G, p->gram_ws, st);
+    launch_syev(p->G, k, p->W, p->Z, p->small, p->scratch, p->iscratch, p->lambda, p->Uh, st);
+    sqrt_eig_kernel<<<static_cast<unsigned>(ceil_div(k, 256)), 256, 0, st>>>(p->lambda, k, S);
+    BSQ_HIP(hipGetLastError());
+    float *Uw_out = p->transposed ? V : U;  // Mw x k
+    float *Vh_out = p->transposed ? U : V;  // Nw x k
+    launch_gemm(false, false, Mw, k, k, Xa, k, p->Uh, k, Uw_out, k, nullptr, nullptr, p->gemm_ws, p->gemm_ws_bytes,
+                st);
+    launch_gemm(false, false, Nw, k, k, Ya, k, p->Uh, k, Vh_out, k, nullptr, nullptr, p->gemm_ws, p->gemm_ws_bytes,
+                st);
+    col_normalize_kernel<<<k, 256, 0, st>>>(Vh_out, Nw, k);
+    BSQ_HIP(hipGetLastError());
+    sign_fix_kernel<<<k, 256, 0, st>>>(U, m, V, n, k);
+    BSQ_HIP(hipGetLastError());
 }
 
 void launch_reconstruct(const float *U, const float *S, const float *V, int m, int n, int k, const float *minuend,
                         float *out, hipStream_t stream) {
     BSQ_REQUIRE(m > 0 && n > 0 && k > 0 && U && S && V && out, "reconstruct: bad arguments");
-    dim3 grid((n + kT - 1) / kT, (m + kT - 1) / kT);
-    reconstruct_simple_kernel<<<grid, dim3(kT, kT), 0, stream>>>(U, S, V, m, n, k, minuend, out);
-    BSQ_HIP(hipGetLastError());
+    // out = (minuend -) (U diag(S)) V^T: A = U with columns scaled by S, B = V^T
+    launch_gemm(false, true, m, n, k, U, k, V, k, out, n, S, minuend, nullptr, 0, stream);
 }
 
 void launch_gaussian_fill(float *out, uint64_t n, uint64_t seed, hipStream_t stream) {

@@ -30,7 +30,7 @@ def test_reference_kats(golden, name):
     np.put_along_axis(expect, idx.astype(np.int64), 0.0, axis=1)
     assert res.tobytes() == expect.tobytes()
     back = B.topk_scatter(idx, val, res, accumulate=True)
-    assert np.array_equal(back, x)
+    assert np.array_equal(back, x, equal_nan=True)
     dense = B.topk_scatter(idx, val, np.full_like(x, 7.0), accumulate=False)
     exp = np.zeros_like(x)
     np.put_along_axis(exp, idx.astype(np.int64), val, axis=1)
