@@ -34,6 +34,9 @@ COMMON = [
 ]
 # Sources whose arithmetic must round operation by operation (bit-exact codecs).
 NO_CONTRACT = {"quant.hip", "topk.hip", "runtime.hip"}
+# Per-file extra flags: the register-resident FP64 factorisations need their
+# fully unrolled loops kept unrolled so the per-thread matrix stays in VGPRs.
+EXTRA = {"linalg.hip": ["-mllvm", "-pragma-unroll-threshold=200000"]}
 
 
 def hipcc() -> str:
@@ -48,6 +51,7 @@ def _compile(src: str) -> str:
     flags = list(COMMON)
     if os.path.basename(src) in NO_CONTRACT:
         flags.append("-ffp-contract=off")
+    flags += EXTRA.get(os.path.basename(src), [])
     cmd = [hipcc(), *flags, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -329,57 +329,69 @@ __global__ void bisect_kernel(const double *__restrict__ d, const double *__rest
     if (t == 0 && e2buf) e2buf[0] = tnorm;
 }
 
-// Solves (T - lam I) x = b in place on b with Gaussian elimination with
-// partial pivoting on the tridiagonal (LAPACK dlagtf / dlagts in spirit);
-// zero pivots are replaced by `tiny`.  Scratch arrays of length k.
-__device__ void trid_solve(const double *d, const double *e, int k, double lam, double tiny, double *b,
-                           double *u0, double *u1, double *u2, double *ml, int *piv) {
-    // factor rows: U has diag u0, super u1, super-super u2
+// LU factorisation with partial pivoting of the tridiagonal T - lam I
+// (LAPACK dlagtf / dlagts in spirit); zero pivots are replaced by `tiny`.
+// Arrays are accessed with a stride so that threads of a wave interleave.
+__device__ void trid_factor(const double *d, const double *e, int k, double lam, double tiny, double *u0,
+                            double *u1, double *u2, double *ml, int *piv, int st) {
     double dcur = d[0] - lam, ecur = (k > 1) ? e[0] : 0.0;
     for (int i = 0; i < k - 1; ++i) {
-        const double sub = e[i];                 // T[i+1][i]
-        const double dn = d[i + 1] - lam;        // T[i+1][i+1]
+        const double sub = e[i];                        // T[i+1][i]
+        const double dn = d[i + 1] - lam;               // T[i+1][i+1]
         const double en = (i + 2 < k) ? e[i + 1] : 0.0;  // T[i+1][i+2]
         if (fabs(dcur) >= fabs(sub)) {
-            piv[i] = 0;
-            double p = dcur;
-            if (p == 0.0) p = tiny;
+            piv[i * st] = 0;
+            const double p = (dcur == 0.0) ? tiny : dcur;
             const double m = sub / p;
-            ml[i] = m;
-            u0[i] = p;
-            u1[i] = ecur;
-            u2[i] = 0.0;
+            ml[i * st] = m;
+            u0[i * st] = p;
+            u1[i * st] = ecur;
+            u2[i * st] = 0.0;
             dcur = dn - m * ecur;
             ecur = en;
         } else {
-            piv[i] = 1;
+            piv[i * st] = 1;
             const double m = dcur / sub;
-            ml[i] = m;
-            u0[i] = sub;
-            u1[i] = dn;
-            u2[i] = en;
+            ml[i * st] = m;
+            u0[i * st] = sub;
+            u1[i * st] = dn;
+            u2[i * st] = en;
             dcur = ecur - m * dn;
             ecur = -m * en;
         }
     }
-    u0[k - 1] = (dcur == 0.0) ? tiny : dcur;
-    // forward: apply L^{-1} P
+    u0[(k - 1) * st] = (fabs(dcur) < tiny) ? (dcur < 0.0 ? -tiny : tiny) : dcur;
+}
+
+__device__ void trid_apply(int k, double tiny, const double *__restrict__ u0, const double *__restrict__ u1,
+                           const double *__restrict__ u2, const double *__restrict__ ml,
+                           const int *__restrict__ piv, int st, double *__restrict__ b, int bst) {
+    // forward: the running pair (cur = b[i], nxt = b[i + 1]) stays in registers
+    double cur = b[0];
     for (int i = 0; i < k - 1; ++i) {
-        if (piv[i]) {
-            const double t = b[i];
-            b[i] = b[i + 1];
-            b[i + 1] = t;
+        double nxt = b[(i + 1) * bst];
+        if (piv[i * st]) {
+            const double t = cur;
+            cur = nxt;
+            nxt = t;
         }
-        b[i + 1] -= ml[i] * b[i];
+        nxt -= ml[i * st] * cur;
+        b[i * bst] = cur;
+        cur = nxt;
     }
-    // backward: U x = b
+    b[(k - 1) * bst] = cur;
+    // backward: x[i] needs x[i + 1], x[i + 2] (registers)
+    double x1 = 0.0, x2 = 0.0;
     for (int i = k - 1; i >= 0; --i) {
-        double s = b[i];
-        if (i + 1 < k) s -= u1[i] * b[i + 1];
-        if (i + 2 < k) s -= u2[i] * b[i + 2];
-        double p = u0[i];
+        double s = b[i * bst];
+        if (i + 1 < k) s -= u1[i * st] * x1;
+        if (i + 2 < k) s -= u2[i * st] * x2;
+        double p = u0[i * st];
         if (fabs(p) < tiny) p = (p < 0.0) ? -tiny : tiny;
-        b[i] = s / p;
+        const double x = s / p;
+        b[i * bst] = x;
+        x2 = x1;
+        x1 = x;
     }
 }
 
@@ -393,7 +405,8 @@ __device__ __forceinline__ double start_entry(int t, int i) {
 }
 
 // Inverse iteration, one thread per eigenvalue: Z[t][0..k) = eigenvector of
-// the tridiagonal for lambda[t].  scratch: 5 k doubles + k ints per thread.
+// the tridiagonal for lambda[t].  Scratch is interleaved across threads
+// (element i of thread t at i * k + t): 5 k doubles + k ints per thread.
 __global__ void invit_kernel(const double *__restrict__ d, const double *__restrict__ e, int k,
                              const double *__restrict__ lambda, const double *__restrict__ tnorm_p,
                              double *__restrict__ Z, double *__restrict__ scratch, int *__restrict__ iscratch) {
@@ -401,19 +414,20 @@ __global__ void invit_kernel(const double *__restrict__ d, const double *__restr
     if (t >= k) return;
     const double tnorm = fmax(tnorm_p[0], DBL_MIN);
     const double tiny = tnorm * DBL_EPSILON;
-    double *b = Z + static_cast<uint64_t>(t) * k;
-    double *sc = scratch + static_cast<uint64_t>(t) * 4 * k;
-    int *piv = iscratch + static_cast<uint64_t>(t) * k;
-    const double lam = lambda[t];
-    for (int i = 0; i < k; ++i) b[i] = start_entry(t, i);
+    const uint64_t kk = static_cast<uint64_t>(k) * k;
+    double *u0 = scratch + t, *u1 = u0 + kk, *u2 = u1 + kk, *ml = u2 + kk, *b = ml + kk;
+    int *piv = iscratch + t;
+    trid_factor(d, e, k, lambda[t], tiny, u0, u1, u2, ml, piv, k);
+    for (int i = 0; i < k; ++i) b[static_cast<uint64_t>(i) * k] = start_entry(t, i);
     for (int it = 0; it < 3; ++it) {
-        trid_solve(d, e, k, lam, tiny, b, sc, sc + k, sc + 2 * k, sc + 3 * k, piv);
+        trid_apply(k, tiny, u0, u1, u2, ml, piv, k, b, k);
         double nrm = 0.0;
-        for (int i = 0; i < k; ++i) nrm = fma(b[i], b[i], nrm);
-        nrm = sqrt(nrm);
-        const double inv = nrm > 0.0 ? 1.0 / nrm : 0.0;
-        for (int i = 0; i < k; ++i) b[i] *= inv;
+        for (int i = 0; i < k; ++i) nrm = fma(b[static_cast<uint64_t>(i) * k], b[static_cast<uint64_t>(i) * k], nrm);
+        const double inv = nrm > 0.0 ? 1.0 / sqrt(nrm) : 0.0;
+        for (int i = 0; i < k; ++i) b[static_cast<uint64_t>(i) * k] *= inv;
     }
+    double *z = Z + static_cast<uint64_t>(t) * k;
+    for (int i = 0; i < k; ++i) z[i] = b[static_cast<uint64_t>(i) * k];
 }
 
 // Re-runs inverse iteration for eigenvalue clusters (gap below
@@ -433,14 +447,17 @@ __global__ void cluster_kernel(const double *__restrict__ d, const double *__res
     int c1 = c0 + 1;
     while (c1 + 1 < k && close(c1)) ++c1;
     const double tiny = tnorm * DBL_EPSILON;
-    double *sc = scratch + static_cast<uint64_t>(c0) * 4 * k;
-    int *piv = iscratch + static_cast<uint64_t>(c0) * k;
+    // private region: the cluster's first index owns rows c0 of the
+    // interleaved scratch planes, used here with stride 1 over a k block
+    double *sc = scratch + 5ull * k * k + static_cast<uint64_t>(c0) * 4 * k;
+    int *piv = iscratch + static_cast<uint64_t>(k) * k + static_cast<uint64_t>(c0) * k;
     for (int t = c0; t <= c1; ++t) {
         double *b = Z + static_cast<uint64_t>(t) * k;
         for (int i = threadIdx.x; i < k; i += blockDim.x) b[i] = start_entry(t + 977, i) - 0.5;
+        if (threadIdx.x == 0) trid_factor(d, e, k, lambda[t], tiny, sc, sc + k, sc + 2 * k, sc + 3 * k, piv, 1);
         __syncthreads();
         for (int it = 0; it < 3; ++it) {
-            if (threadIdx.x == 0) trid_solve(d, e, k, lambda[t], tiny, b, sc, sc + k, sc + 2 * k, sc + 3 * k, piv);
+            if (threadIdx.x == 0) trid_apply(k, tiny, sc, sc + k, sc + 2 * k, sc + 3 * k, piv, 1, b, 1);
             __syncthreads();
             for (int pass = 0; pass < 2; ++pass) {
                 for (int s = c0; s < t; ++s) {
@@ -491,6 +508,459 @@ __global__ void backtransform_kernel(const double *__restrict__ W, const double 
     for (int i = lane; i < k; i += 64) Uh[static_cast<uint64_t>(i) * k + t] = static_cast<float>(z[i]);
 }
 
+// ===========================================================================
+// Register-resident versions for k <= 256: the lower triangle of the k x k
+// FP64 matrix lives in the VGPRs of one 1024-thread workgroup, distributed
+// 2-D cyclically: thread (ty, tx) = (tid / 32, tid % 32) owns the elements
+// (a*32 + ty, b*32 + tx), a >= b, of the padded NB*32 matrix.  Every
+// elimination step is one rank-1 (or rank-2) register update plus two LDS
+// broadcasts, so no step touches L2.
+// ===========================================================================
+__device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
+
+// Cholesky G + shift I = L L^T, then in-place L^{-1} (Gauss-Jordan on [L | I]
+// with the right part overwriting the consumed columns of L).  VT virtual
+// 32-thread rows per physical thread row (1024 / VT threads).
+template <int NB, int VT>
+__global__ __launch_bounds__(kBig / VT) void chol_inv_reg_kernel(const double *__restrict__ G, int k,
+                                                                  float *__restrict__ Linv, int *__restrict__ status) {
+    constexpr int NE = NB * (NB + 1) / 2;
+    constexpr int KP = NB * 32;
+    constexpr int NT = kBig / VT, TYS = 32 / VT;
+    __shared__ double lcol[KP], rrow[KP];
+    __shared__ double red[NT / 64];
+    __shared__ double piv;
+    __shared__ int broke;
+    const int tid = threadIdx.x, tx = tid & 31, ty0 = tid >> 5;
+    double r[VT][NE];
+    for (int i = tid; i < KP; i += NT) lcol[i] = rrow[i] = 0.0;
+    double dmax = 0.0;
+    for (int i = tid; i < k; i += NT) dmax = fmax(dmax, fabs(G[static_cast<uint64_t>(i) * k + i]));
+    dmax = block_max(dmax, red);
+    const double tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
+    double shift = 0.0;
+    int attempt = 0;
+    bool identity = false;
+    for (;; ++attempt) {
+#pragma unroll
+        for (int h = 0; h < VT; ++h)
+#pragma unroll
+            for (int a = 0; a < NB; ++a)
+#pragma unroll
+                for (int b = 0; b <= a; ++b) {
+                    const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
+                    double v = 0.0;
+                    if (i >= c) {
+                        if (i < k && c < k) v = G[static_cast<uint64_t>(i) * k + c] + (i == c ? shift : 0.0);
+                        else if (i == c) v = 1.0;  // padding: identity
+                    }
+                    r[h][tri(a, b)] = v;
+                }
+        if (tid == 0) broke = 0;
+        __syncthreads();
+        bool stop = false;
+#pragma unroll
+        for (int jb = 0; jb < NB; ++jb) {
+            for (int jt = 0; jt < 32 && !stop; ++jt) {
+                const int j = jb * 32 + jt;
+                if (tx == jt) {
+#pragma unroll
+                    for (int h = 0; h < VT; ++h)
+                        if (ty0 + h * TYS == jt) {
+                            const double d = r[h][tri(jb, jb)];
+                            if (!(d > tiny)) {
+                                broke = 1;
+                            } else {
+                                const double dj = sqrt(d);
+                                r[h][tri(jb, jb)] = dj;
+                                piv = dj;
+                            }
+                        }
+                }
+                __syncthreads();
+                if (broke) {
+                    stop = true;
+                    break;
+                }
+                if (tx == jt) {
+                    const double inv = 1.0 / piv;
+#pragma unroll
+                    for (int h = 0; h < VT; ++h) {
+                        const int ty = ty0 + h * TYS;
+#pragma unroll
+                        for (int a = jb; a < NB; ++a)
+                            if (a > jb || ty > jt) {
+                                const double v = r[h][tri(a, jb)] * inv;
+                                r[h][tri(a, jb)] = v;
+                                lcol[a * 32 + ty] = v;
+                            }
+                    }
+                }
+                __syncthreads();
+                // trailing update; the column mask keeps columns <= j intact,
+                // rows <= j only touch the unused upper halves
+#pragma unroll
+                for (int b = jb; b < NB; ++b) {
+                    const double lc = lcol[b * 32 + tx];
+                    const bool colok = (b > jb) || (tx > jt);
+#pragma unroll
+                    for (int h = 0; h < VT; ++h)
+#pragma unroll
+                        for (int a = b; a < NB; ++a) {
+                            const double upd = fma(-lcol[a * 32 + ty0 + h * TYS], lc, r[h][tri(a, b)]);
+                            r[h][tri(a, b)] = colok ? upd : r[h][tri(a, b)];  // select: stale LDS never leaks
+                        }
+                }
+            }
+        }
+        if (!stop) break;
+        if (attempt >= 6 || dmax == 0.0) {
+            identity = true;
+            break;
+        }
+        shift = (shift == 0.0) ? dmax * 1e-12 * static_cast<double>(k) : shift * 100.0;
+        __syncthreads();
+    }
+    if (identity) {
+#pragma unroll
+        for (int h = 0; h < VT; ++h)
+#pragma unroll
+            for (int a = 0; a < NB; ++a)
+#pragma unroll
+                for (int b = 0; b <= a; ++b)
+                    r[h][tri(a, b)] = (a * 32 + ty0 + h * TYS == b * 32 + tx) ? 1.0 : 0.0;
+    }
+    __syncthreads();
+    // in-place inverse
+#pragma unroll
+    for (int jb = 0; jb < NB; ++jb) {
+        for (int jt = 0; jt < 32; ++jt) {
+            const int j = jb * 32 + jt;
+            if (tx == jt) {
+#pragma unroll
+                for (int h = 0; h < VT; ++h)
+                    if (ty0 + h * TYS == jt) {
+                        const double p = 1.0 / r[h][tri(jb, jb)];
+                        r[h][tri(jb, jb)] = p;
+                        piv = p;
+                        rrow[j] = p;
+                    }
+            }
+            __syncthreads();
+            const double p = piv;
+#pragma unroll
+            for (int h = 0; h < VT; ++h) {
+                const int ty = ty0 + h * TYS;
+                if (ty == jt) {  // row j of the inverse so far, scaled
+#pragma unroll
+                    for (int b = 0; b <= jb; ++b) {
+                        const int c = b * 32 + tx;
+                        if (c < j) {
+                            const double v = r[h][tri(jb, b)] * p;
+                            r[h][tri(jb, b)] = v;
+                            rrow[c] = v;
+                        }
+                    }
+                }
+                if (tx == jt) {  // column j of L below the diagonal (consumed now)
+#pragma unroll
+                    for (int a = jb; a < NB; ++a)
+                        if (a > jb || ty > jt) lcol[a * 32 + ty] = r[h][tri(a, jb)];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int b = 0; b <= jb; ++b) {
+                const double rc = rrow[b * 32 + tx];
+                const bool colok = (b < jb) || (tx <= jt);
+                const bool cj = (b == jb) && (tx == jt);
+#pragma unroll
+                for (int h = 0; h < VT; ++h) {
+                    const int ty = ty0 + h * TYS;
+#pragma unroll
+                    for (int a = jb; a < NB; ++a) {
+                        const bool rowok = (a > jb) || (ty > jt);  // rows <= j are final
+                        const double old = cj ? 0.0 : r[h][tri(a, b)];
+                        const double upd = fma(-lcol[a * 32 + ty], rc, old);
+                        r[h][tri(a, b)] = (rowok && colok) ? upd : r[h][tri(a, b)];
+                    }
+                }
+            }
+        }
+    }
+    // output: lower part from registers, zeros above
+    for (uint64_t t = tid; t < static_cast<uint64_t>(k) * k; t += NT) {
+        const int i = static_cast<int>(t / k), c = static_cast<int>(t % k);
+        if (c > i) Linv[t] = 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < VT; ++h)
+#pragma unroll
+        for (int a = 0; a < NB; ++a)
+#pragma unroll
+            for (int b = 0; b <= a; ++b) {
+                const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
+                if (i < k && c < k && i >= c)
+                    Linv[static_cast<uint64_t>(i) * k + c] = static_cast<float>(r[h][tri(a, b)]);
+            }
+    if (tid == 0 && status) status[0] = attempt;
+}
+
+// Householder tridiagonalisation with the lower triangle in registers.
+// Writes d, e, tau and the reflectors row-wise: H[j][i] = v_j[i] (zero for
+// i <= j, one at i = j + 1).
+template <int NB, int VT>
+__global__ __launch_bounds__(kBig / VT) void sytrd_reg_kernel(const double *__restrict__ G, int k,
+                                                               double *__restrict__ d, double *__restrict__ e,
+                                                               double *__restrict__ tau, double *__restrict__ H) {
+    constexpr int NE = NB * (NB + 1) / 2;
+    constexpr int KP = NB * 32;
+    constexpr int NT = kBig / VT, TYS = 32 / VT;
+    __shared__ double xs[KP], vs[KP], ws[KP], prow[KP];
+    __shared__ double part[32][KP + 1];
+    __shared__ double red[NT / 64];
+    __shared__ double s_tau;
+    const int tid = threadIdx.x, tx = tid & 31, ty0 = tid >> 5;
+    double r[VT][NE];
+#pragma unroll
+    for (int h = 0; h < VT; ++h)
+#pragma unroll
+        for (int a = 0; a < NB; ++a)
+#pragma unroll
+            for (int b = 0; b <= a; ++b) {
+                const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
+                r[h][tri(a, b)] = (i >= c && i < k && c < k) ? G[static_cast<uint64_t>(i) * k + c] : 0.0;
+            }
+    const int steps = k - 2;  // reflectors j = 0 .. k-3
+#pragma unroll
+    for (int jb = 0; jb < NB; ++jb) {
+        for (int jt = 0; jt < 32; ++jt) {
+            const int j = jb * 32 + jt;
+            if (j >= steps) break;
+            // column j below the diagonal -> xs
+            if (tx == jt) {
+#pragma unroll
+                for (int h = 0; h < VT; ++h) {
+                    const int ty = ty0 + h * TYS;
+#pragma unroll
+                    for (int a = jb; a < NB; ++a)
+                        if (a > jb || ty > jt) xs[a * 32 + ty] = r[h][tri(a, jb)];
+                    if (ty == jt) d[j] = r[h][tri(jb, jb)];
+                }
+            }
+            __syncthreads();
+            // reflector (wave 0): v = [1, x(j+2:) / (alpha - beta)], tau
+            if (tid < 64) {
+                double sig = 0.0;
+                for (int i = j + 2 + tid; i < k; i += 64) sig = fma(xs[i], xs[i], sig);
+                for (int off = 32; off >= 1; off >>= 1) sig += __shfl_xor(sig, off);
+                const double alpha = xs[j + 1];
+                double t = 0.0, beta = alpha, scal = 0.0;
+                if (sig > 0.0) {
+                    const double nrm = sqrt(fma(alpha, alpha, sig));
+                    beta = (alpha >= 0.0) ? -nrm : nrm;
+                    t = (beta - alpha) / beta;
+                    scal = 1.0 / (alpha - beta);
+                }
+                for (int i = tid; i < KP; i += 64) {
+                    double v = 0.0;
+                    if (i == j + 1) v = 1.0;
+                    else if (i > j + 1 && i < k) v = xs[i] * scal;
+                    vs[i] = v;
+                    if (i < k) H[static_cast<uint64_t>(j) * k + i] = v;
+                }
+                if (tid == 0) {
+                    e[j] = beta;
+                    tau[j] = t;
+                    s_tau = t;
+                }
+            }
+            __syncthreads();
+            const double t = s_tau;
+            if (t == 0.0) continue;  // uniform
+            // p = A' v from the lower triangle.  v vanishes at indices <= j,
+            // so stale entries in processed columns contribute nothing to
+            // p[i > j]; p[<= j] is discarded.
+#pragma unroll
+            for (int b = jb; b < NB; ++b) {
+                const double vb = vs[b * 32 + tx];
+#pragma unroll
+                for (int h = 0; h < VT; ++h) {
+                    const int ty = ty0 + h * TYS;
+                    double sc = 0.0;
+#pragma unroll
+                    for (int a = b; a < NB; ++a)
+                        if (a > b || ty > tx) sc = fma(r[h][tri(a, b)], vs[a * 32 + ty], sc);
+                    part[ty][b * 32 + tx] = sc;
+                }
+                (void)vb;
+            }
+#pragma unroll
+            for (int h = 0; h < VT; ++h) {
+                const int ty = ty0 + h * TYS;
+#pragma unroll
+                for (int a = jb; a < NB; ++a) {
+                    double sa = 0.0;
+#pragma unroll
+                    for (int b = jb; b <= a; ++b)
+                        if (a > b || ty >= tx) sa = fma(r[h][tri(a, b)], vs[b * 32 + tx], sa);
+                    for (int off = 16; off >= 1; off >>= 1) sa += __shfl_xor(sa, off, 32);
+                    if (tx == 0) prow[a * 32 + ty] = sa;
+                }
+            }
+            __syncthreads();
+            double pt = 0.0;
+            for (int q = tid; q < KP; q += NT) {
+                if (q > j) {
+                    double s = prow[q];
+                    for (int y = 0; y < 32; ++y) s += part[y][q];
+                    ws[q] = s * t;
+                } else {
+                    ws[q] = 0.0;
+                }
+            }
+            __syncthreads();
+            for (int q = tid; q < KP; q += NT) pt = fma(ws[q], vs[q], pt);
+            const double pv = block_sum(pt, red);
+            for (int q = tid; q < KP; q += NT) ws[q] = (q > j) ? ws[q] - 0.5 * t * pv * vs[q] : 0.0;
+            __syncthreads();
+            // rank-2 update; v and w vanish at indices <= j
+#pragma unroll
+            for (int b = jb; b < NB; ++b) {
+                const double vb = vs[b * 32 + tx], wb = ws[b * 32 + tx];
+#pragma unroll
+                for (int h = 0; h < VT; ++h) {
+                    const int ty = ty0 + h * TYS;
+#pragma unroll
+                    for (int a = b; a < NB; ++a) {
+                        const double va = vs[a * 32 + ty], wa = ws[a * 32 + ty];
+                        r[h][tri(a, b)] = fma(-va, wb, fma(-wa, vb, r[h][tri(a, b)]));
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // trailing 2 x 2 (or 1 x 1) block
+    const int j2 = k - 2;
+#pragma unroll
+    for (int h = 0; h < VT; ++h)
+#pragma unroll
+        for (int a = 0; a < NB; ++a)
+#pragma unroll
+            for (int b = 0; b <= a; ++b) {
+                const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
+                if (i == c && i >= (j2 > 0 ? j2 : 0) && i < k) d[i] = r[h][tri(a, b)];
+                if (j2 >= 0 && i == j2 + 1 && c == j2) e[j2] = r[h][tri(a, b)];
+            }
+    if (tid == 0) {
+        if (k >= 2) tau[k - 2] = 0.0;
+        tau[k - 1] = 0.0;
+    }
+}
+
+// Bisection by multisection: one wave per eigenvalue, 63 interior points per
+// pass.  lambda[t] = t-th largest eigenvalue.
+__global__ __launch_bounds__(64) void multisect_kernel(const double *__restrict__ d, const double *__restrict__ e,
+                                                        int k, double *__restrict__ lambda, double *__restrict__ tnorm_out) {
+    extern __shared__ double sm[];  // d[k], e2[k]
+    double *sd = sm, *se2 = sm + k;
+    __shared__ double bounds[2];
+    const int lane = threadIdx.x;
+    double lo = 1e300, hi = -1e300, emax = 0.0;
+    for (int i = lane; i < k; i += 64) {
+        sd[i] = d[i];
+        const double ei = (i + 1 < k) ? e[i] : 0.0;
+        se2[i] = ei * ei;
+        const double r = (i > 0 ? fabs(e[i - 1]) : 0.0) + fabs(ei);
+        lo = fmin(lo, d[i] - r);
+        hi = fmax(hi, d[i] + r);
+        emax = fmax(emax, ei * ei);
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        lo = fmin(lo, __shfl_xor(lo, off));
+        hi = fmax(hi, __shfl_xor(hi, off));
+        emax = fmax(emax, __shfl_xor(emax, off));
+    }
+    __syncthreads();
+    const double tnorm = fmax(fabs(lo), fabs(hi));
+    const double pivmin = DBL_MIN * fmax(1.0, emax) * 4.0;
+    lo -= 2.0 * tnorm * DBL_EPSILON * k + pivmin;
+    hi += 2.0 * tnorm * DBL_EPSILON * k + pivmin;
+    const int t = blockIdx.x;
+    const int target = k - 1 - t;  // ascending index of the wanted eigenvalue
+    double a = lo, b = hi;
+    for (int pass = 0; pass < 40; ++pass) {
+        if (b - a <= 2.0 * DBL_EPSILON * fmax(fabs(a), fabs(b)) + pivmin) break;
+        const double h = (b - a) / 64.0;
+        const double x = a + h * (lane + 1);  // lanes 0..62 interior, lane 63 = b
+        const int cnt = (lane < 63) ? sturm_count(sd, se2, k, x, pivmin) : k + 1;
+        // smallest point whose count exceeds target bounds the eigenvalue from above
+        const unsigned long long above = __ballot(cnt > target);
+        const int first = __ffsll(above) - 1;  // always found (lane 63)
+        const double nb = a + h * (first + 1);
+        const double na = (first == 0) ? a : a + h * first;
+        if (!(nb < b) && !(na > a)) break;
+        a = na;
+        b = fmin(nb, b);
+    }
+    if (lane == 0) {
+        lambda[t] = 0.5 * (a + b);
+        if (t == 0 && tnorm_out) tnorm_out[0] = tnorm;
+    }
+}
+
+// Back-transformation with row-wise reflectors H[j][*]: u_t = H_0 ... H_{k-3} z_t.
+// One wave per eigenvector with z in registers (KPL = ceil(k / 64) values
+// per lane); reflector rows are staged through LDS 16 at a time and shared
+// by the 16 waves of the workgroup.
+template <int KPL>
+__global__ __launch_bounds__(1024) void backtransform_rows_kernel(const double *__restrict__ H,
+                                                                  const double *__restrict__ tau, int k,
+                                                                  const double *__restrict__ Z,
+                                                                  float *__restrict__ Uh) {
+    constexpr int RB = 16;
+    __shared__ double hs[RB][KPL * 64];
+    __shared__ double ts[RB];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 16 + wave;
+    double z[KPL];
+#pragma unroll
+    for (int m = 0; m < KPL; ++m) {
+        const int i = lane + 64 * m;
+        z[m] = (t < k && i < k) ? Z[static_cast<uint64_t>(t) * k + i] : 0.0;
+    }
+    for (int j0 = k - 3; j0 >= 0; j0 -= RB) {
+        const int jl = max(0, j0 - RB + 1);  // rows jl .. j0, applied from j0 down
+        __syncthreads();
+        for (int q = threadIdx.x; q < RB * KPL * 64; q += blockDim.x) {
+            const int rr = q / (KPL * 64), i = q % (KPL * 64);
+            const int j = j0 - rr;
+            hs[rr][i] = (j >= jl && i < k) ? H[static_cast<uint64_t>(j) * k + i] : 0.0;
+        }
+        if (threadIdx.x < RB) ts[threadIdx.x] = (j0 - (int)threadIdx.x >= jl) ? tau[j0 - threadIdx.x] : 0.0;
+        __syncthreads();
+        for (int rr = 0; rr <= j0 - jl; ++rr) {
+            const double tj = ts[rr];
+            if (tj == 0.0) continue;
+            double s = 0.0;
+#pragma unroll
+            for (int m = 0; m < KPL; ++m) s = fma(hs[rr][lane + 64 * m], z[m], s);
+            for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+            s *= tj;
+#pragma unroll
+            for (int m = 0; m < KPL; ++m) z[m] = fma(-s, hs[rr][lane + 64 * m], z[m]);
+        }
+    }
+    if (t < k) {
+#pragma unroll
+        for (int m = 0; m < KPL; ++m) {
+            const int i = lane + 64 * m;
+            if (i < k) Uh[static_cast<uint64_t>(i) * k + t] = static_cast<float>(z[m]);
+        }
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -519,34 +989,79 @@ void launch_gram(const float *X, int M, int k, int ld, double *G, double *worksp
     BSQ_HIP(hipGetLastError());
 }
 
+template <int NB>
+static void chol_reg(const double *G, int k, float *Linv, int *status, hipStream_t stream) {
+    constexpr int VT = 1;
+    chol_inv_reg_kernel<NB, VT><<<1, kBig / VT, 0, stream>>>(G, k, Linv, status);
+}
+
 void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(k) * sizeof(double);
-    BSQ_REQUIRE(lds <= 64 * 1024, "chol_inv: rank too large");
-    chol_inv_kernel<<<1, kBig, lds, stream>>>(G, k, W, Linv, status);
+    const int nb = static_cast<int>(ceil_div(k, 32));
+    switch (nb) {
+        case 1: chol_reg<1>(G, k, Linv, status, stream); break;
+        case 2: chol_reg<2>(G, k, Linv, status, stream); break;
+        case 3: chol_reg<3>(G, k, Linv, status, stream); break;
+        case 4: chol_reg<4>(G, k, Linv, status, stream); break;
+        case 5: chol_reg<5>(G, k, Linv, status, stream); break;
+        case 6: chol_reg<6>(G, k, Linv, status, stream); break;
+        case 7: chol_reg<7>(G, k, Linv, status, stream); break;
+        case 8: chol_reg<8>(G, k, Linv, status, stream); break;
+        default: {
+            const size_t lds = static_cast<size_t>(k) * sizeof(double);
+            BSQ_REQUIRE(lds <= 64 * 1024, "chol_inv: rank too large");
+            chol_inv_kernel<<<1, kBig, lds, stream>>>(G, k, W, Linv, status);
+        }
+    }
     BSQ_HIP(hipGetLastError());
+}
+
+template <int NB>
+static void sytrd_reg(const double *G, int k, double *d, double *e, double *tau, double *H, hipStream_t stream) {
+    constexpr int VT = 1;
+    sytrd_reg_kernel<NB, VT><<<1, kBig / VT, 0, stream>>>(G, k, d, e, tau, H);
 }
 
 // Eigen-decomposition of the symmetric G (k x k FP64): lambda descending,
 // Uh[i][t] = component i of eigenvector t (FP32).  `W` k*k doubles, `Z`
-// k*k doubles, `small` >= 4k + 8 doubles, `scratch` 4*k*k doubles,
-// `iscratch` k*k ints.
+// k*k doubles, `small` >= 4k + 8 doubles, `scratch` 9*k*k doubles,
+// `iscratch` 2*k*k ints.
 void launch_syev(const double *G, int k, double *W, double *Z, double *small, double *scratch, int *iscratch,
                  double *lambda, float *Uh, hipStream_t stream) {
     BSQ_REQUIRE(k >= 1 && static_cast<size_t>(2 * k) * sizeof(double) <= 64 * 1024, "syev: rank too large");
     double *d = small, *e = small + k, *tau = small + 2 * k, *tn = small + 3 * k;
-    BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));
-    sytrd_kernel<<<1, kBig, 2 * k * sizeof(double), stream>>>(W, k, d, e, tau);
+    const int nb = static_cast<int>(ceil_div(k, 32));
+    bool reg = true;
+    switch (nb) {
+        case 1: sytrd_reg<1>(G, k, d, e, tau, W, stream); break;
+        case 2: sytrd_reg<2>(G, k, d, e, tau, W, stream); break;
+        case 3: sytrd_reg<3>(G, k, d, e, tau, W, stream); break;
+        case 4: sytrd_reg<4>(G, k, d, e, tau, W, stream); break;
+        case 5: sytrd_reg<5>(G, k, d, e, tau, W, stream); break;
+        case 6: sytrd_reg<6>(G, k, d, e, tau, W, stream); break;
+        case 7: sytrd_reg<7>(G, k, d, e, tau, W, stream); break;
+        case 8: sytrd_reg<8>(G, k, d, e, tau, W, stream); break;
+        default:
+            reg = false;
+            BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice,
+                                   stream));
+            sytrd_kernel<<<1, kBig, 2 * k * sizeof(double), stream>>>(W, k, d, e, tau);
+    }
     BSQ_HIP(hipGetLastError());
-    const int bthreads = 256;
-    bisect_kernel<<<static_cast<unsigned>(ceil_div(k, bthreads)), bthreads, 2 * k * sizeof(double), stream>>>(
-        d, e, k, lambda, tn);
+    multisect_kernel<<<k, 64, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);
     BSQ_HIP(hipGetLastError());
     invit_kernel<<<static_cast<unsigned>(ceil_div(k, 64)), 64, 0, stream>>>(d, e, k, lambda, tn, Z, scratch,
                                                                            iscratch);
     BSQ_HIP(hipGetLastError());
     cluster_kernel<<<k, 256, 0, stream>>>(d, e, k, lambda, tn, Z, scratch, iscratch);
     BSQ_HIP(hipGetLastError());
-    backtransform_kernel<<<static_cast<unsigned>(ceil_div(k, 4)), 256, 0, stream>>>(W, tau, k, Z, Uh);
+    if (reg) {
+        const unsigned g = static_cast<unsigned>(ceil_div(k, 16));
+        if (k <= 64) backtransform_rows_kernel<1><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
+        else if (k <= 128) backtransform_rows_kernel<2><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
+        else if (k <= 192) backtransform_rows_kernel<3><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
+        else backtransform_rows_kernel<4><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
+    } else
+        backtransform_kernel<<<static_cast<unsigned>(ceil_div(k, 4)), 256, 0, stream>>>(W, tau, k, Z, Uh);
     BSQ_HIP(hipGetLastError());
 }
 

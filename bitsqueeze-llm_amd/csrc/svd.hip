@@ -209,9 +209,9 @@ SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
         p->W = alloc<double>(k * k);
         p->Z = alloc<double>(k * k);
         p->small = alloc<double>(4 * k + 8);
-        p->scratch = alloc<double>(4 * k * k);
+        p->scratch = alloc<double>(9 * k * k);
         p->lambda = alloc<double>(k);
-        p->iscratch = alloc<int>(k * k);
+        p->iscratch = alloc<int>(2 * k * k);
         p->status = alloc<int>(4);
         const uint64_t gw = std::max(gram_workspace_bytes(p->Mw, p->k), gram_workspace_bytes(p->Nw, p->k));
         p->gram_ws = alloc<double>(gw / sizeof(double) + 1);
