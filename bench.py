@@ -6,8 +6,21 @@ A step is one device-resident compress (bsq_device_compress) followed by one
 device-resident decompress (bsq_device_decompress) of a synthetic FP32
 matrix that is already in HBM; `value` is GB/s of FP32 input
 (4*rows*cols*K / time of the K timed steps).  Prints one JSON line with the
-roofline figure of the dominant kernel (timed live with HIP events on the
-runtime stream) and the reference's CPU codec timed on this host.
+roofline figure of the dominant kernel and the reference's CPU codec timed on
+this host.
+
+Dominant kernel: on the SVD workloads, the FP32-MFMA GEMM that touches the
+full matrix; the one timed is the low-rank reconstruction
+U diag(S) V^T (gemm_mfma_kernel<false, true, true>), bracketed with HIP
+events on the runtime stream inside the timed steps (2 * rows * cols * rank
+flops per launch, twice per step).  On the direct workloads, the NF4 / NF4_DQ
+encode of the full matrix (read 4N bytes, write the section), timed with HIP
+events on the runtime stream after the timed steps.  `traffic` is read from
+the committed rocprofv3 --pmc summary for that kernel and workload, when one
+exists.
+
+    python bench.py --calibrate-copy   # also launches the plain copy kernel
+                                       # (for rocprofv3 --pmc calibration runs)
 """
 from __future__ import annotations
 
@@ -15,6 +28,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import re
 import sys
 import time
 
@@ -104,6 +118,48 @@ def time_dominant_kernel(wl, rows, cols, dsrc, stream, reps=20):
     return name, ms, alg_bytes
 
 
+def abi_leg(dsrc, ddst, n, reps=5):
+    """Wall clock of the reference ABI calls bitsqz_llm_compress (device input,
+    host packed object: includes the payload D2H) + bitsqz_llm_decompress
+    (includes the payload H2D); returns (GB/s of FP32 input, ms per step)."""
+    L = B.lib()
+    times = []
+    for i in range(reps + 1):
+        out = C.POINTER(B.PackedHeader)()
+        prof = B.Profile()
+        t0 = time.perf_counter()
+        B.check(L.bsq_compress(dsrc.ptr, C.byref(out), C.byref(prof)), "bitsqz_llm_compress")
+        B.check(L.bsq_decompress(C.cast(out, C.c_void_p), ddst.ptr, n), "bitsqz_llm_decompress")
+        dt = time.perf_counter() - t0
+        L.bsq_free(C.cast(out, C.c_void_p))
+        if i:
+            times.append(dt)
+    ms = 1e3 * float(np.median(times))
+    return 4.0 * n / (ms * 1e-3) / 1e9, ms
+
+
+def committed_traffic(kernel_tag: str, workload: str):
+    """HBM bytes per launch of `kernel_tag` at `workload` from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated),
+    or None when no such summary exists."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_{workload}_pmc.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\s*=\s*(\d+)", open(path).read(), re.M)
+    return int(m.group(1)) if m else None
+
+
+def roofline_time_ms(rows, cols, svd, nit, q, err_on, payload_bytes):
+    """T_roof of the whole step: MFMA time of the GEMMs over the m x n matrix
+    (2 N q (2 + 2 it) + 2 N q (1 + [error top-k])) for the SVD path, HBM time
+    of 8N + 2P bytes for the direct path."""
+    n = rows * cols
+    if svd >= 1:
+        flops = 2.0 * n * q * (2 + 2 * nit) + 2.0 * n * q * (1 + (1 if err_on else 0))
+        return flops / (FP32_MFMA_PEAK_TFLOPS * 1e12) * 1e3
+    return (8.0 * n + 2.0 * payload_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
+
+
 def cpu_baseline(x, direct, budget_s=12.0):
     """The reference's legacy OpenMP NF4 / NF4_DQ codec (compiled from the
     reference's own sources into oracle/_ref) on a bounded row sample of the
@@ -116,7 +172,7 @@ def cpu_baseline(x, direct, budget_s=12.0):
     method = direct if direct != B.QUANT_NONE else B.NF4
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
     ref_so = os.path.join(ROOT, "oracle", "_ref", "libref_nf4.so")
-    rows = max(64, min(x.shape[0], 512))
+    rows = x.shape[0]  # the whole matrix, repeated for about budget_s seconds
     sample = np.ascontiguousarray(x[:rows])
     n = sample.size
     nb, nc = (n + 63) // 64, (n + 1) // 2
@@ -156,13 +212,13 @@ def cpu_baseline(x, direct, budget_s=12.0):
     while True:
         once()
         reps += 1
-        if time.perf_counter() - t0 > budget_s or reps >= 200:
+        if time.perf_counter() - t0 > budget_s:
             break
     dt = (time.perf_counter() - t0) / reps
     gbs = 4 * n / dt / 1e9
     label = "NF4" if method == B.NF4 else "NF4_DQ"
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"legacy {label} compress+decompress of the first {rows} rows ({rows}x{x.shape[1]}), "
+            "sample": f"legacy {label} compress+decompress of the full {rows}x{x.shape[1]} matrix, "
                       f"{reps} reps in {reps * dt:.1f} s; the reference has no CPU top-k / SVD path"}
 
 
@@ -173,6 +229,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="headline", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only; the multi-GPU design (row shards, one "
@@ -201,6 +258,8 @@ def main():
     for _ in range(args.warmup):
         p = step()
     B.device_synchronize()
+    if svd >= 1:
+        B.kernel_timer_start()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         p = step()
@@ -209,17 +268,44 @@ def main():
     ms_per_step = dt / args.steps * 1e3
     value = 4.0 * n * args.steps / dt / 1e9
     print(f"bench: timed {args.steps} steps, {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
-
     # correctness spot check of the last step against the input (reconstruction error)
     out = ddst.download(np.float32, n).reshape(rows, cols)
     rel = float(np.linalg.norm(out - x) / max(np.linalg.norm(x), 1e-30))
 
     stream = B.runtime_stream()
-    kname, kms, kbytes = time_dominant_kernel(wl, rows, cols, dsrc, stream)
-    achieved = kbytes / (kms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kname,
-                "avg_ms": round(kms, 5), "alg_bytes": kbytes}
+    if svd >= 1:
+        total_ms, launches = B.kernel_timer_stop()
+        kms = total_ms / max(launches, 1)
+        kflops = 2.0 * rows * cols * q
+        achieved = kflops / (kms * 1e-3) / 1e12
+        tag = "gemm_reconstruct"
+        roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                    "traffic": committed_traffic(tag, args.workload),
+                    "kernel": "gemm_mfma_kernel<false, true, true> (U diag(S) V^T, FP32 MFMA)",
+                    "avg_ms": round(kms, 5), "launches": launches, "alg_flops": kflops}
+    else:
+        kname, kms, kbytes = time_dominant_kernel(wl, rows, cols, dsrc, stream)
+        achieved = kbytes / (kms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": committed_traffic("quant_encode", args.workload), "kernel": kname,
+                    "avg_ms": round(kms, 5), "alg_bytes": kbytes}
+
+    t_roof = roofline_time_ms(rows, cols, svd, nit, q, re > 0, packed_payload_bytes(p, bool(re > 0)))
+    pipeline = {"t_roof_ms": round(t_roof, 4), "frac_of_roofline": round(t_roof / ms_per_step, 4)}
+
+    abi_gbs, abi_ms = abi_leg(dsrc, ddst, n)
+    abi = {"value": round(abi_gbs, 3), "unit": "GB/s", "ms_per_step": round(abi_ms, 4),
+           "what": "bitsqz_llm_compress + bitsqz_llm_decompress wall clock (payload D2H / H2D included), "
+                   "median of 5"}
+
+    if args.calibrate_copy:
+        # known-size copy for rocprofv3 --pmc calibration (FETCH_SIZE / WRITE_SIZE per byte)
+        for _ in range(3):
+            B.check(B.lib().bsq_copy_kernel(dsrc.ptr, ddst.ptr, 4 * n, stream), "copy kernel")
+        B.device_synchronize()
+        print(f"bench: copy kernel calibration, {4 * n} bytes read + written per launch", file=sys.stderr)
 
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -230,6 +316,8 @@ def main():
                    "svd_uv_format": uv, "svd_s_format": s, "quantization_only_format": direct,
                    "input": "device-resident", "rel_frobenius_error": round(rel, 6)},
         "roofline": roofline,
+        "pipeline_roofline": pipeline,
+        "abi_pcie_inclusive": abi,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(x, direct if svd < 1 else uv)

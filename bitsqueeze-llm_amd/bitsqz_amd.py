@@ -126,6 +126,9 @@ def lib():
         "bsq_event_destroy": (i32, [P]),
         "bsq_event_record": (i32, [P, P]),
         "bsq_event_elapsed_ms": (i32, [P, P, C.POINTER(f32)]),
+        "bsq_kernel_timer_start": (i32, []),
+        "bsq_copy_kernel": (i32, [P, P, u64, P]),
+        "bsq_kernel_timer_stop": (i32, [C.POINTER(C.c_double), C.POINTER(i32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -198,6 +201,18 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+def kernel_timer_start() -> None:
+    """Bracket every reconstruction GEMM of the pipelines with HIP events."""
+    check(lib().bsq_kernel_timer_start(), "kernel timer start")
+
+
+def kernel_timer_stop() -> tuple[float, int]:
+    """Stop bracketing; returns (summed kernel ms, launches) since the start."""
+    ms, n = C.c_double(), C.c_int()
+    check(lib().bsq_kernel_timer_stop(C.byref(ms), C.byref(n)), "kernel timer stop")
+    return ms.value, n.value
 
 
 def device_count() -> int:

@@ -141,7 +141,10 @@ struct KMajor {
     }
 };
 
-template <bool TA, bool TB>
+// RECON: the low-rank reconstruction form (column scale on op(A), optional
+// minuend), instantiated separately so the power-iteration GEMMs carry no
+// epilogue branches and profiles tell the two apart.
+template <bool TA, bool TB, bool RECON>
 __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
     constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
     constexpr int FM = WM / 16, FN = WN / 16;
@@ -164,10 +167,8 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
     typename std::conditional<TB, KContig<BN>, KMajor<BN>>::type tb;
 
     auto load = [&](int k0) {
-        if constexpr (!TA) ta.load(g.A, g.lda, m0, g.M, k0, kend, g.vec_a, g.a_colscale);
-        else ta.load(g.A, g.lda, m0, g.M, k0, kend, g.vec_a, g.a_colscale);
-        if constexpr (!TB) tb.load(g.B, g.ldb, n0, g.N, k0, kend, g.vec_b, nullptr);
-        else tb.load(g.B, g.ldb, n0, g.N, k0, kend, g.vec_b, nullptr);
+        ta.load(g.A, g.lda, m0, g.M, k0, kend, g.vec_a, RECON ? g.a_colscale : nullptr);
+        tb.load(g.B, g.ldb, n0, g.N, k0, kend, g.vec_b, nullptr);
     };
 
     int buf = 0;
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
                 if (gi < g.M && gj < g.N) {
                     const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
                     const float v = acc[i][j][r];
-                    C[e] = g.minuend ? g.minuend[e] - v : v;
+                    C[e] = (RECON && g.minuend) ? g.minuend[e] - v : v;
                 }
             }
 }
@@ -271,7 +272,7 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
                  int ldc, const float *a_colscale, const float *minuend, float *workspace, uint64_t workspace_bytes,
                  hipStream_t stream) {
     BSQ_REQUIRE(M > 0 && N > 0 && K > 0 && A && B && C, "gemm: bad arguments");
-    int splits = minuend ? 1 : choose_splits(M, N, K);
+    int splits = (minuend || a_colscale) ? 1 : choose_splits(M, N, K);
     if (splits > 1 && (!workspace || static_cast<uint64_t>(splits) * M * N * sizeof(float) > workspace_bytes))
         splits = 1;
     GemmArgs g{};
@@ -297,10 +298,14 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
         g.split_stride = 0;
     }
     dim3 grid(static_cast<unsigned>(ceil_div(N, BN)), static_cast<unsigned>(ceil_div(M, BM)), splits);
-    if (!ta && !tb) gemm_mfma_kernel<false, false><<<grid, kThreads, 0, stream>>>(g);
-    else if (ta && !tb) gemm_mfma_kernel<true, false><<<grid, kThreads, 0, stream>>>(g);
-    else if (!ta && tb) gemm_mfma_kernel<false, true><<<grid, kThreads, 0, stream>>>(g);
-    else gemm_mfma_kernel<true, true><<<grid, kThreads, 0, stream>>>(g);
+    const bool recon = a_colscale || minuend;
+    if (recon) {
+        BSQ_REQUIRE(!ta && tb, "gemm: column scale / minuend only in the A * B^T form");
+        gemm_mfma_kernel<false, true, true><<<grid, kThreads, 0, stream>>>(g);
+    } else if (!ta && !tb) gemm_mfma_kernel<false, false, false><<<grid, kThreads, 0, stream>>>(g);
+    else if (ta && !tb) gemm_mfma_kernel<true, false, false><<<grid, kThreads, 0, stream>>>(g);
+    else if (!ta && tb) gemm_mfma_kernel<false, true, false><<<grid, kThreads, 0, stream>>>(g);
+    else gemm_mfma_kernel<true, true, false><<<grid, kThreads, 0, stream>>>(g);
     BSQ_HIP(hipGetLastError());
     if (splits > 1) {
         const uint64_t total = static_cast<uint64_t>(M) * N;

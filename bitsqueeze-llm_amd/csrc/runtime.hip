@@ -171,6 +171,58 @@ struct Runtime {
 Runtime g_comp;
 Runtime g_decomp;
 
+// Plain 16-byte-per-lane copy: the known-size reference against which HBM
+// counters of the other kernels are calibrated (bytes read = bytes written =
+// 16 * n4).
+__global__ void copy_f32x4_kernel(const float4 *__restrict__ src, float4 *__restrict__ dst, uint64_t n4) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        dst[i] = src[i];
+}
+
+// Optional HIP-event bracketing of the reconstruction GEMM launches inside the
+// compress / decompress pipelines (off unless bsq_kernel_timer_start is
+// called): measures that kernel live, on the stream it runs on.
+struct KernelTimer {
+    bool on = false;
+    std::vector<hipEvent_t> ev;  // pairs: ev[2i] before, ev[2i+1] after
+    size_t used = 0;             // pairs recorded since the last read
+    template <class F>
+    void run(hipStream_t st, F &&launch) {
+        if (!on) {
+            launch();
+            return;
+        }
+        if (2 * used + 2 > ev.size()) {
+            hipEvent_t a = nullptr, b = nullptr;
+            BSQ_HIP(hipEventCreate(&a));
+            if (hipEventCreate(&b) != hipSuccess) {
+                (void)hipEventDestroy(a);
+                fail("kernel timer: hipEventCreate failed");
+            }
+            ev.push_back(a);
+            ev.push_back(b);
+        }
+        BSQ_HIP(hipEventRecord(ev[2 * used], st));
+        launch();
+        BSQ_HIP(hipEventRecord(ev[2 * used + 1], st));
+        ++used;
+    }
+    void read(double *total_ms, int *launches) {
+        double t = 0.0;
+        for (size_t i = 0; i < used; ++i) {
+            BSQ_HIP(hipEventSynchronize(ev[2 * i + 1]));
+            float ms = 0.0f;
+            BSQ_HIP(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
+            t += ms;
+        }
+        *total_ms = t;
+        *launches = static_cast<int>(used);
+        used = 0;
+    }
+};
+KernelTimer g_recon_timer;
+
 bool ratio_is_valid(float r) { return std::isfinite(r) && r >= 0.0f && r <= 1.0f; }
 bool method_is_valid(int m) { return m == kMethodNone || m == kMethodNF4 || m == kMethodNF4DQ; }
 bool uses_quant(const Runtime &rt) {
@@ -368,7 +420,9 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
         BSQ_HIP(hipEventRecord(rt.ev[4], st));
         if (te.capacity > 0) {
             // reconstruct + subtract fused (src/bitsqz_llm.cu:1141-1163)
-            launch_reconstruct(U.dense, S.dense, V.dense, rows, cols, rt.q, residual, rt.d_err, st);
+            g_recon_timer.run(st, [&] {
+                launch_reconstruct(U.dense, S.dense, V.dense, rows, cols, rt.q, residual, rt.d_err, st);
+            });
             BSQ_HIP(hipEventRecord(rt.ev[5], st));
             TopkArgs a;
             a.a = rt.d_err;
@@ -496,7 +550,7 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
                 dense[i] = sc.dense;
             }
         }
-        launch_reconstruct(dense[0], dense[1], dense[2], rows, cols, q, nullptr, d_dst, st);
+        g_recon_timer.run(st, [&] { launch_reconstruct(dense[0], dense[1], dense[2], rows, cols, q, nullptr, d_dst, st); });
     } else {
         const uint64_t N = static_cast<uint64_t>(rows) * cols;
         if (P.d_dense[SEC_DIRECT]) {
@@ -1180,6 +1234,37 @@ int bsq_event_record(void *event, void *stream) {
     return guarded(
         [&] { BSQ_HIP(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream))); });
 }
+int bsq_copy_kernel(const void *d_src, void *d_dst, uint64_t bytes, void *stream) {
+    return guarded([&] {
+        BSQ_REQUIRE(d_src && d_dst && bytes % 16 == 0, "copy kernel: null pointer or size not a multiple of 16");
+        BSQ_REQUIRE((reinterpret_cast<uintptr_t>(d_src) | reinterpret_cast<uintptr_t>(d_dst)) % 16 == 0,
+                    "copy kernel: pointers must be 16-byte aligned");
+        const uint64_t n4 = bytes / 16;
+        if (n4 == 0) return;
+        uint64_t grid = ceil_div(n4, 256);
+        const uint64_t cap = static_cast<uint64_t>(cu_count()) * 16;
+        if (grid > cap) grid = cap;
+        copy_f32x4_kernel<<<static_cast<unsigned>(grid), 256, 0, static_cast<hipStream_t>(stream)>>>(
+            static_cast<const float4 *>(d_src), static_cast<float4 *>(d_dst), n4);
+        BSQ_HIP(hipGetLastError());
+    });
+}
+
+int bsq_kernel_timer_start(void) {
+    return guarded([&] {
+        g_recon_timer.on = true;
+        g_recon_timer.used = 0;
+    });
+}
+
+int bsq_kernel_timer_stop(double *total_ms, int *launches) {
+    return guarded([&] {
+        BSQ_REQUIRE(total_ms && launches, "null output");
+        g_recon_timer.on = false;
+        g_recon_timer.read(total_ms, launches);
+    });
+}
+
 int bsq_event_elapsed_ms(void *start, void *stop, float *ms) {
     return guarded([&] {
         BSQ_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)));

@@ -47,7 +47,7 @@ static const float kLevels[16] = {
 ORACLE_API const float *oracle_nf4_levels(void) { return kLevels; }
 
 /* Nearest code with first-minimum tie break: linear scan with strict '<'
- * (nf4_impl.cpp:73-86; identical in nf4_dq_impl.cpp:295-308 and
+ * (nf4_impl.cpp:73-86; identical in nf4_dq_impl.cpp:131-144 and
  * quantization_cuda.cu:43-58).  Non-finite input maps to 0.0. */
 ORACLE_API uint8_t oracle_nf4_code(float x) {
     if (!isfinite(x)) x = 0.0f;
@@ -125,7 +125,7 @@ ORACLE_API void oracle_nf4_decompress(const float *scales, const uint8_t *codes,
     }
 }
 
-/* FP8 E4M3 encode as the reference writes it (nf4_dq_impl.cpp:247-276):
+/* FP8 E4M3 encode as the reference writes it (nf4_dq_impl.cpp:83-112):
  * non-finite -> +-448, clamp to 448, frexpf split, round-half-even mantissa,
  * sub-normal branch clamps the mantissa to 7. */
 ORACLE_API uint8_t oracle_e4m3_encode(float x) {
@@ -154,7 +154,7 @@ ORACLE_API uint8_t oracle_e4m3_encode(float x) {
     return (uint8_t)((sign << 7) | ((ef & 0xF) << 3) | (mf & 0x7));
 }
 
-/* FP8 E4M3 decode (nf4_dq_impl.cpp:278-293); code 0x7F decodes to 480. */
+/* FP8 E4M3 decode (nf4_dq_impl.cpp:114-129); code 0x7F decodes to 480. */
 ORACLE_API float oracle_e4m3_decode(uint8_t v) {
     const int sign = (v >> 7) & 1, ef = (v >> 3) & 0xF, mf = v & 7;
     float r;
@@ -163,7 +163,7 @@ ORACLE_API float oracle_e4m3_decode(uint8_t v) {
     return sign ? -r : r;
 }
 
-/* NF4_DQ compress (nf4_dq_impl.cpp:326-389): per-block absmax (zero block ->
+/* NF4_DQ compress (nf4_dq_impl.cpp:162-242): per-block absmax (zero block ->
  * 1), one global dq = max/448 (max over finite block scales; 0 -> 1), E4M3
  * code of absmax/dq per block, effective scale dq*E4M3^-1(code) (0 or
  * non-finite -> 1), then NF4 encode with its reciprocal. */
@@ -179,7 +179,7 @@ ORACLE_API void oracle_nf4dq_compress(const float *x, uint64_t n, float *dq_out,
         const float m = block_absmax(x, start, remain);
         absmax[b] = (m > 0.0f) ? m : 1.0f;
     }
-    /* choose_dq_scale, nf4_dq_impl.cpp:314-324 */
+    /* choose_dq_scale, nf4_dq_impl.cpp:150-160 */
     float gmax = 0.0f;
     for (uint64_t i = 0; i < nb; ++i) {
         const float v = absmax[i];
@@ -203,7 +203,7 @@ ORACLE_API void oracle_nf4dq_compress(const float *x, uint64_t n, float *dq_out,
     free(absmax);
 }
 
-/* NF4_DQ decompress (nf4_dq_impl.cpp:408-439): out = (dq*E4M3^-1(s_b)) * level. */
+/* NF4_DQ decompress (nf4_dq_impl.cpp:244-275): out = (dq*E4M3^-1(s_b)) * level. */
 ORACLE_API void oracle_nf4dq_decompress(float dq, const uint8_t *scale_codes,
                                         const uint8_t *codes, uint64_t n, float *out) {
     const uint64_t bs = 64, nb = (n + bs - 1) / bs;

@@ -37,7 +37,7 @@ __attribute__((visibility("default"))) int ref_nf4_decompress(const float *scale
     return rc;
 }
 
-// nf4_dq_compress (nf4_dq_impl.cpp:391-406).
+// nf4_dq_compress (nf4_dq_impl.cpp:227-242).
 __attribute__((visibility("default"))) int ref_nf4dq_compress(const float *x, unsigned long long n,
                                                               float *dq, unsigned char *scale_codes,
                                                               unsigned char *codes) {
@@ -50,7 +50,7 @@ __attribute__((visibility("default"))) int ref_nf4dq_compress(const float *x, un
     return 0;
 }
 
-// nf4_dq_decompress (nf4_dq_impl.cpp:408-439).
+// nf4_dq_decompress (nf4_dq_impl.cpp:244-275).
 __attribute__((visibility("default"))) int ref_nf4dq_decompress(float dq,
                                                                 const unsigned char *scale_codes,
                                                                 const unsigned char *codes,
