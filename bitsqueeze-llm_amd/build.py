@@ -36,7 +36,8 @@ COMMON = [
 NO_CONTRACT = {"quant.hip", "topk.hip", "runtime.hip"}
 # Per-file extra flags: the register-resident FP64 factorisations need their
 # fully unrolled loops kept unrolled so the per-thread matrix stays in VGPRs.
-EXTRA = {"linalg.hip": ["-mllvm", "-pragma-unroll-threshold=200000"]}
+EXTRA = {"linalg.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
+         "chol.hip": ["-mllvm", "-pragma-unroll-threshold=200000"]}
 
 
 def hipcc() -> str:

@@ -1,0 +1,343 @@
+// Blocked Cholesky factorisation and triangular inverse for CholeskyQR
+// (k x k FP64 Gram matrices, k <= 256).
+//
+//   chol_blocked_kernel   one workgroup of 1024 lanes; the lower triangle of
+//                         the padded KP x KP matrix (KP = 32 * NB) lives in
+//                         registers, lane (ty, tx) holding element
+//                         (32a + ty, 32b + tx) of every lower 32 x 32 block.
+//                         Right-looking by 32-column panels: one wave
+//                         factors and inverts the diagonal block, all lanes
+//                         form the panel L_ij = A_ij L_jj^{-T} and apply the
+//                         rank-32 trailing update from an LDS copy of the
+//                         panel.  8 panel steps replace 256 column steps, so
+//                         the workgroup synchronises ~50 times instead of
+//                         ~1500.  Breakdown (pivot <= 1e-15 max|G_ii|) restarts
+//                         with a diagonal shift, as the unblocked version does.
+//   trinv_kernel          L^{-1} by blocked forward substitution, 8 columns
+//                         per workgroup, so the inverse is spread over
+//                         k / 8 CUs instead of one.  Writes B = L^{-T} in
+//                         FP32 row-major (B[r][c] = L^{-1}[c][r]) so that the
+//                         orthonormal basis is the plain product Q = X B.
+//
+// The reference orthonormalises with Householder QR (cuSOLVER geqrf/orgqr,
+// modules/svd_lowrank_cuda/src/svd_lowrank_cuda.cu:250-282); any basis of the
+// same column space serves the range finder.
+#include "bsq_internal.hpp"
+
+namespace bsq {
+namespace {
+
+constexpr int kCholThreads = 1024;
+
+__device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
+
+// value of `v` in lane `src` (src wave-uniform), via two scalar reads
+__device__ __forceinline__ double lane_value(double v, int src) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), src));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), src));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// v if bit == 1, +0.0 if bit == 0 (bit is 0 or 1), by masking the bit pattern:
+// lane-dependent selects would materialise one lane mask per call site and
+// the fully unrolled loops below would keep dozens of them live.
+__device__ __forceinline__ double keep_if(double v, unsigned bit) {
+    const unsigned long long m = 0ull - static_cast<unsigned long long>(bit);
+    return __longlong_as_double(static_cast<long long>(static_cast<unsigned long long>(__double_as_longlong(v)) & m));
+}
+
+// Opaque copy: the compiler must assume the value changed, so lane-dependent
+// index and mask arithmetic derived from it stays inside the loop body that
+// uses it instead of being hoisted (and kept live across the whole
+// factorisation, which spills).
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// value of `v` in lane `src` (src may differ per lane), via the LDS crossbar
+__device__ __forceinline__ double lane_fetch(double v, int src) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(u & 0xffffffffu)));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(u >> 32)));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// Orders one wave's LDS accesses: wait for its outstanding LDS operations and
+// keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ double wg_max(double v, double *red) {
+    for (int off = 32; off >= 1; off >>= 1) v = fmax(v, __shfl_xor(v, off));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double s = red[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) s = fmax(s, red[w]);
+    return s;
+}
+
+// Lout: KP x KP row-major (lower blocks written: L; diagonal blocks with
+// zeros above the diagonal).  LIout: NB blocks of 32 x 32, the inverses of
+// the diagonal blocks of L (zeros above the diagonal).  status[0]: number of
+// shifted restarts (7 = gave up, L = I).
+template <int NB>
+__global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double *__restrict__ G, int k,
+                                                                     double *__restrict__ Lout,
+                                                                     double *__restrict__ LIout,
+                                                                     int *__restrict__ status) {
+    constexpr int KP = NB * 32, NE = NB * (NB + 1) / 2, PR = (NB > 1) ? (NB - 1) * 32 : 1;
+    __shared__ double Dg[32][33];                          // diagonal block (row-major)
+    __shared__ double LT[32][33];                          // L_jj column-major: LT[s][t] = L[t][s]
+    __shared__ __attribute__((aligned(16))) double LI[32][34];  // L_jj^{-1}, row-major
+    __shared__ __attribute__((aligned(16))) double P[PR][34];   // panel rows below the diagonal block
+    __shared__ double stash[NE][64];                       // wave 0's registers during its solo phase
+    __shared__ double colb[32];                            // column broadcast of the 32 x 32 factorisation
+    __shared__ double red[kCholThreads / 64];
+    __shared__ int broke;
+
+    double dmax = 0.0;
+    for (int i = threadIdx.x; i < k; i += kCholThreads) dmax = fmax(dmax, fabs(G[static_cast<uint64_t>(i) * k + i]));
+    dmax = wg_max(dmax, red);
+    const double tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
+    double shift = 0.0;
+    int attempt = 0;
+    bool identity = false;
+    double r[NE];
+    for (;; ++attempt) {
+        int tid = opaque(static_cast<int>(threadIdx.x));
+        int tx = tid & 31, ty = tid >> 5;
+#pragma unroll
+        for (int a = 0; a < NB; ++a)
+#pragma unroll
+            for (int b = 0; b <= a; ++b) {
+                // branch-free: G (+ shift on the diagonal) inside, identity in the padding
+                const int i = a * 32 + ty, c = b * 32 + tx;
+                const unsigned inside = (static_cast<unsigned>(i - k) >> 31) & (static_cast<unsigned>(c - k) >> 31);
+                const unsigned diag = 1u - min(1u, static_cast<unsigned>(i ^ c));
+                const double g = G[inside ? static_cast<uint64_t>(i) * k + c : 0];
+                r[tri(a, b)] = keep_if(g, inside) +
+                               static_cast<double>(diag) * (inside ? shift : 1.0);
+            }
+        if (tid == 0) broke = 0;
+        bool failed = false;
+#pragma unroll
+        for (int jb = 0; jb < NB; ++jb) {
+            if (failed) break;
+            tid = opaque(static_cast<int>(threadIdx.x));
+            tx = tid & 31;
+            ty = tid >> 5;
+            const int lane = tid & 63, wave = tid >> 6;
+            __syncthreads();  // readers of Dg / P from the previous step are done
+            Dg[ty][tx] = r[tri(jb, jb)];
+#pragma unroll
+            for (int a = jb + 1; a < NB; ++a) P[(a - jb - 1) * 32 + ty][tx] = r[tri(a, jb)];
+            __syncthreads();
+            if (wave == 0) {
+                // free wave 0's registers for the 32 x 32 factorisation
+#pragma unroll
+                for (int e = 0; e < NE; ++e) stash[e][lane] = r[e];
+                // the compiler may not forward the stash into the reload below (that
+                // would keep r live through the factorisation)
+                asm volatile("" ::: "memory");
+                // 8 x 8 lane grid, lane (lr, lc) holding the 4 x 4 sub-blocks
+                // a = A[4lr.., 4lc..] and x = X[4lr.., 4lc..] of the diagonal
+                // block and of its inverse (X starts as I).  Step t: scale column
+                // t of A and row t of X by 1/sqrt(pivot), fetch the four column-t
+                // values of this lane's rows and columns and the four row-t values
+                // of X with lane permutes, then rank-1 update A's trailing columns
+                // and X's trailing rows (Gauss-Jordan on [L | I] fused into the
+                // factorisation).
+                const int lr = lane >> 3, lc = lane & 7;
+                double a[4][4], x[4][4];
+                const double on_diag = static_cast<double>(1u - min(1u, static_cast<unsigned>(lr ^ lc)));
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        a[p][q] = Dg[4 * lr + p][4 * lc + q];
+                        x[p][q] = (p == q) ? on_diag : 0.0;
+                    }
+                bool bad = false;
+#pragma unroll
+                for (int t = 0; t < 32; ++t) {
+                    const int tb = t >> 2, tq = t & 3;
+                    const double dtt = lane_value(a[tq][tq], tb * 9);
+                    bad = bad || !(dtt > tiny);
+                    const double inv = rsqrt(dtt);
+                    const double fc = (lc == tb) ? inv : 1.0, fr = (lr == tb) ? inv : 1.0;
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) a[p][tq] *= fc;  // column t of L (row t: sqrt(pivot))
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) x[tq][q] *= fr;  // row t of L^{-1}
+                    double lrow[4], lcol[4], xrow[4];
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        lrow[p] = lane_fetch(a[p][tq], lr * 8 + tb);  // L[4lr + p][t]
+                        lcol[p] = lane_fetch(a[p][tq], lc * 8 + tb);  // L[4lc + p][t]
+                        xrow[p] = lane_fetch(x[tq][p], tb * 8 + lc);  // X[t][4lc + p]
+                    }
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        // only columns c > t of A and rows i > t of X change
+                        const double cb = keep_if(lcol[p], static_cast<unsigned>(t - (4 * lc + p)) >> 31);
+                        const double rb = keep_if(lrow[p], static_cast<unsigned>(t - (4 * lr + p)) >> 31);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            a[q][p] = fma(-lrow[q], cb, a[q][p]);
+                            x[p][q] = fma(-rb, xrow[q], x[p][q]);
+                        }
+                    }
+                }
+                if (bad && lane == 0) broke = 1;
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        LI[4 * lr + p][4 * lc + q] = x[p][q];  // exactly zero above the diagonal
+                        LIout[static_cast<uint64_t>(jb) * 1024 + (4 * lr + p) * 32 + 4 * lc + q] = x[p][q];
+                    }
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int e = 0; e < NE; ++e) r[e] = stash[e][lane];
+            }
+            __syncthreads();
+            if (broke) {
+                failed = true;
+                break;
+            }
+
+            // panel: L_ij = A_ij L_jj^{-T}, element (32a + ty, 32 jb + tx)
+            double acc[NB];
+#pragma unroll
+            for (int a = 0; a < NB; ++a) acc[a] = 0.0;
+#pragma unroll 1
+            for (int t = 0; t < 32; t += 2) {
+                const double2 li = *reinterpret_cast<const double2 *>(&LI[tx][t]);
+#pragma unroll
+                for (int a = jb + 1; a < NB; ++a) {
+                    const double2 pa = *reinterpret_cast<const double2 *>(&P[(a - jb - 1) * 32 + ty][t]);
+                    acc[a] = fma(pa.x, li.x, fma(pa.y, li.y, acc[a]));
+                }
+            }
+            __syncthreads();  // every lane has read the A panel
+#pragma unroll
+            for (int a = jb + 1; a < NB; ++a) {
+                r[tri(a, jb)] = acc[a];
+                P[(a - jb - 1) * 32 + ty][tx] = acc[a];
+                Lout[static_cast<uint64_t>(a * 32 + ty) * KP + jb * 32 + tx] = acc[a];
+            }
+            __syncthreads();
+            // trailing update A_ab -= L_aj L_bj^T for jb < b <= a
+            if (jb + 1 < NB) {
+#pragma unroll 1
+                for (int t = 0; t < 32; ++t) {
+                    double rv[NB];
+#pragma unroll
+                    for (int a = jb + 1; a < NB; ++a) rv[a] = P[(a - jb - 1) * 32 + ty][t];
+#pragma unroll
+                    for (int b = jb + 1; b < NB; ++b) {
+                        const double cv = P[(b - jb - 1) * 32 + tx][t];
+#pragma unroll
+                        for (int a = b; a < NB; ++a) r[tri(a, b)] = fma(-rv[a], cv, r[tri(a, b)]);
+                    }
+                }
+            }
+        }
+        if (!failed) break;
+        if (attempt >= 6 || dmax == 0.0) {
+            identity = true;
+            break;
+        }
+        shift = (shift == 0.0) ? dmax * 1e-12 * static_cast<double>(k) : shift * 100.0;
+        __syncthreads();
+    }
+    const int tid = threadIdx.x;
+    if (identity) {
+        __syncthreads();
+        for (int t = tid; t < KP * KP; t += kCholThreads) {
+            const int i = t / KP, c = t % KP;
+            if (c <= i) Lout[t] = (i == c) ? 1.0 : 0.0;
+        }
+        for (int t = tid; t < NB * 1024; t += kCholThreads) {
+            const int i = (t & 1023) >> 5, c = t & 31;
+            LIout[t] = (i == c) ? 1.0 : 0.0;
+        }
+    }
+    if (tid == 0 && status) status[0] = attempt;
+}
+
+// Columns c0 .. c0+7 of L^{-1}, block row by block row:
+//   X_cb = LI_cb[:, cols];  X_i = -LI_i * sum_{t=cb}^{i-1} L_it X_t
+// Output B = L^{-T} (k x k FP32 row-major): B[c][r] = L^{-1}[r][c].
+template <int NB>
+__global__ __launch_bounds__(256) void trinv_kernel(const double *__restrict__ Lin, const double *__restrict__ LIin,
+                                                    int k, float *__restrict__ B) {
+    constexpr int KP = NB * 32;
+    __shared__ double X[KP][8];
+    __shared__ double S[32][8];
+    const int c0 = blockIdx.x * 8, cb = c0 >> 5, co = c0 & 31;
+    const int tid = threadIdx.x, rr = tid >> 3, j = tid & 7;
+    X[cb * 32 + rr][j] = LIin[static_cast<uint64_t>(cb) * 1024 + rr * 32 + co + j];
+    __syncthreads();
+    for (int i = cb + 1; i < NB; ++i) {
+        const double *lrow = Lin + static_cast<uint64_t>(i * 32 + rr) * KP;
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+        for (int col = cb * 32; col < i * 32; col += 4) {
+            s0 = fma(lrow[col + 0], X[col + 0][j], s0);
+            s1 = fma(lrow[col + 1], X[col + 1][j], s1);
+            s2 = fma(lrow[col + 2], X[col + 2][j], s2);
+            s3 = fma(lrow[col + 3], X[col + 3][j], s3);
+        }
+        S[rr][j] = (s0 + s1) + (s2 + s3);
+        __syncthreads();
+        const double *li = LIin + static_cast<uint64_t>(i) * 1024 + rr * 32;
+        double x = 0.0;
+        for (int u = 0; u <= rr; ++u) x = fma(li[u], S[u][j], x);
+        X[i * 32 + rr][j] = -x;
+        __syncthreads();
+    }
+    for (int t = tid; t < 8 * k; t += 256) {
+        const int jj = t / k, r = t % k, c = c0 + jj;
+        if (c < k) B[static_cast<uint64_t>(c) * k + r] = (r >= cb * 32) ? static_cast<float>(X[r][jj]) : 0.0f;
+    }
+}
+
+template <int NB>
+void chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream) {
+    double *L = Lbuf, *LI = Lbuf + static_cast<uint64_t>(NB) * 32 * NB * 32;
+    chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, status);
+    BSQ_HIP(hipGetLastError());
+    trinv_kernel<NB><<<static_cast<unsigned>(ceil_div(k, 8)), 256, 0, stream>>>(L, LI, k, B);
+    BSQ_HIP(hipGetLastError());
+}
+
+}  // namespace
+
+// FP64 doubles needed by launch_chol_blocked's L buffer for rank k.
+uint64_t chol_blocked_buffer_doubles(int k) {
+    const uint64_t nb = ceil_div(k, 32);
+    return nb * 32 * nb * 32 + nb * 1024;
+}
+
+bool chol_blocked_supported(int k) { return k >= 1 && k <= 256; }
+
+// G = L L^T (with shifted restarts on breakdown) and B = L^{-T} (FP32,
+// k x k row-major), so that X B has orthonormal columns when G = X^T X.
+void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream) {
+    BSQ_REQUIRE(chol_blocked_supported(k), "chol: rank outside the blocked kernel's range");
+    switch (ceil_div(k, 32)) {
+        case 1: chol_blocked<1>(G, k, Lbuf, B, status, stream); break;
+        case 2: chol_blocked<2>(G, k, Lbuf, B, status, stream); break;
+        case 3: chol_blocked<3>(G, k, Lbuf, B, status, stream); break;
+        case 4: chol_blocked<4>(G, k, Lbuf, B, status, stream); break;
+        case 5: chol_blocked<5>(G, k, Lbuf, B, status, stream); break;
+        case 6: chol_blocked<6>(G, k, Lbuf, B, status, stream); break;
+        case 7: chol_blocked<7>(G, k, Lbuf, B, status, stream); break;
+        default: chol_blocked<8>(G, k, Lbuf, B, status, stream); break;
+    }
+}
+
+}  // namespace bsq

@@ -2,7 +2,8 @@
 //
 //   gram      G = X^T X (FP32 X, FP64 products and sums), split over rows
 //   chol_inv  G = L L^T (FP64, shifted retry on breakdown) and L^{-1} as FP32
-//             (CholeskyQR: Q = X L^{-T})
+//             (CholeskyQR: Q = X L^{-T}); unblocked, for ranks above 256 (the
+//             blocked kernels for k <= 256 are in chol.hip)
 //   syev      G = U diag(lambda) U^T (FP64): Householder tridiagonalisation,
 //             bisection with Sturm counts, inverse iteration (clusters
 //             re-orthogonalised), back-transformation
@@ -13,6 +14,7 @@
 // Gram matrices are formed exactly in FP64 from the FP32 factors.
 #include "bsq_internal.hpp"
 
+#include <algorithm>
 #include <cfloat>
 
 namespace bsq {
@@ -430,6 +432,39 @@ __global__ void invit_kernel(const double *__restrict__ d, const double *__restr
     for (int i = 0; i < k; ++i) z[i] = b[static_cast<uint64_t>(i) * k];
 }
 
+// The same inverse iteration with every per-eigenvalue array in LDS: lane j
+// (< P) of a one-wave workgroup handles eigenvalue blockIdx.x * P + j, its
+// element i at i * P + j.  The recurrences are sequential per eigenvalue, so
+// what bounds them is the latency of each step's loads: LDS instead of L2.
+__global__ __launch_bounds__(64) void invit_lds_kernel(const double *__restrict__ d, const double *__restrict__ e,
+                                                       int k, int P, const double *__restrict__ lambda,
+                                                       const double *__restrict__ tnorm_p, double *__restrict__ Z) {
+    extern __shared__ double sm[];
+    const uint64_t kp = static_cast<uint64_t>(k) * P;
+    double *u0 = sm, *u1 = u0 + kp, *u2 = u1 + kp, *ml = u2 + kp, *b = ml + kp, *ds = b + kp, *es = ds + k;
+    int *piv = reinterpret_cast<int *>(es + k);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+        ds[i] = d[i];
+        es[i] = (i + 1 < k) ? e[i] : 0.0;
+    }
+    __syncthreads();
+    const int j = threadIdx.x, t = blockIdx.x * P + j;
+    if (j >= P || t >= k) return;  // no barrier below
+    const double tnorm = fmax(tnorm_p[0], DBL_MIN);
+    const double tiny = tnorm * DBL_EPSILON;
+    trid_factor(ds, es, k, lambda[t], tiny, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P);
+    for (int i = 0; i < k; ++i) b[i * P + j] = start_entry(t, i);
+    for (int it = 0; it < 3; ++it) {
+        trid_apply(k, tiny, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, b + j, P);
+        double nrm = 0.0;
+        for (int i = 0; i < k; ++i) nrm = fma(b[i * P + j], b[i * P + j], nrm);
+        const double inv = nrm > 0.0 ? 1.0 / sqrt(nrm) : 0.0;
+        for (int i = 0; i < k; ++i) b[i * P + j] *= inv;
+    }
+    double *z = Z + static_cast<uint64_t>(t) * k;
+    for (int i = 0; i < k; ++i) z[i] = b[i * P + j];
+}
+
 // Re-runs inverse iteration for eigenvalue clusters (gap below
 // 1e-9 * ||T||), one workgroup per cluster, orthogonalising each member
 // against the earlier members after every solve.
@@ -517,194 +552,6 @@ __global__ void backtransform_kernel(const double *__restrict__ W, const double 
 // broadcasts, so no step touches L2.
 // ===========================================================================
 __device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
-
-// Cholesky G + shift I = L L^T, then in-place L^{-1} (Gauss-Jordan on [L | I]
-// with the right part overwriting the consumed columns of L).  VT virtual
-// 32-thread rows per physical thread row (1024 / VT threads).
-template <int NB, int VT>
-__global__ __launch_bounds__(kBig / VT) void chol_inv_reg_kernel(const double *__restrict__ G, int k,
-                                                                  float *__restrict__ Linv, int *__restrict__ status) {
-    constexpr int NE = NB * (NB + 1) / 2;
-    constexpr int KP = NB * 32;
-    constexpr int NT = kBig / VT, TYS = 32 / VT;
-    __shared__ double lcol[KP], rrow[KP];
-    __shared__ double red[NT / 64];
-    __shared__ double piv;
-    __shared__ int broke;
-    const int tid = threadIdx.x, tx = tid & 31, ty0 = tid >> 5;
-    double r[VT][NE];
-    for (int i = tid; i < KP; i += NT) lcol[i] = rrow[i] = 0.0;
-    double dmax = 0.0;
-    for (int i = tid; i < k; i += NT) dmax = fmax(dmax, fabs(G[static_cast<uint64_t>(i) * k + i]));
-    dmax = block_max(dmax, red);
-    const double tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
-    double shift = 0.0;
-    int attempt = 0;
-    bool identity = false;
-    for (;; ++attempt) {
-#pragma unroll
-        for (int h = 0; h < VT; ++h)
-#pragma unroll
-            for (int a = 0; a < NB; ++a)
-#pragma unroll
-                for (int b = 0; b <= a; ++b) {
-                    const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
-                    double v = 0.0;
-                    if (i >= c) {
-                        if (i < k && c < k) v = G[static_cast<uint64_t>(i) * k + c] + (i == c ? shift : 0.0);
-                        else if (i == c) v = 1.0;  // padding: identity
-                    }
-                    r[h][tri(a, b)] = v;
-                }
-        if (tid == 0) broke = 0;
-        __syncthreads();
-        bool stop = false;
-#pragma unroll
-        for (int jb = 0; jb < NB; ++jb) {
-            for (int jt = 0; jt < 32 && !stop; ++jt) {
-                const int j = jb * 32 + jt;
-                if (tx == jt) {
-#pragma unroll
-                    for (int h = 0; h < VT; ++h)
-                        if (ty0 + h * TYS == jt) {
-                            const double d = r[h][tri(jb, jb)];
-                            if (!(d > tiny)) {
-                                broke = 1;
-                            } else {
-                                const double dj = sqrt(d);
-                                r[h][tri(jb, jb)] = dj;
-                                piv = dj;
-                            }
-                        }
-                }
-                __syncthreads();
-                if (broke) {
-                    stop = true;
-                    break;
-                }
-                if (tx == jt) {
-                    const double inv = 1.0 / piv;
-#pragma unroll
-                    for (int h = 0; h < VT; ++h) {
-                        const int ty = ty0 + h * TYS;
-#pragma unroll
-                        for (int a = jb; a < NB; ++a)
-                            if (a > jb || ty > jt) {
-                                const double v = r[h][tri(a, jb)] * inv;
-                                r[h][tri(a, jb)] = v;
-                                lcol[a * 32 + ty] = v;
-                            }
-                    }
-                }
-                __syncthreads();
-                // trailing update; the column mask keeps columns <= j intact,
-                // rows <= j only touch the unused upper halves
-#pragma unroll
-                for (int b = jb; b < NB; ++b) {
-                    const double lc = lcol[b * 32 + tx];
-                    const bool colok = (b > jb) || (tx > jt);
-#pragma unroll
-                    for (int h = 0; h < VT; ++h)
-#pragma unroll
-                        for (int a = b; a < NB; ++a) {
-                            const double upd = fma(-lcol[a * 32 + ty0 + h * TYS], lc, r[h][tri(a, b)]);
-                            r[h][tri(a, b)] = colok ? upd : r[h][tri(a, b)];  // select: stale LDS never leaks
-                        }
-                }
-            }
-        }
-        if (!stop) break;
-        if (attempt >= 6 || dmax == 0.0) {
-            identity = true;
-            break;
-        }
-        shift = (shift == 0.0) ? dmax * 1e-12 * static_cast<double>(k) : shift * 100.0;
-        __syncthreads();
-    }
-    if (identity) {
-#pragma unroll
-        for (int h = 0; h < VT; ++h)
-#pragma unroll
-            for (int a = 0; a < NB; ++a)
-#pragma unroll
-                for (int b = 0; b <= a; ++b)
-                    r[h][tri(a, b)] = (a * 32 + ty0 + h * TYS == b * 32 + tx) ? 1.0 : 0.0;
-    }
-    __syncthreads();
-    // in-place inverse
-#pragma unroll
-    for (int jb = 0; jb < NB; ++jb) {
-        for (int jt = 0; jt < 32; ++jt) {
-            const int j = jb * 32 + jt;
-            if (tx == jt) {
-#pragma unroll
-                for (int h = 0; h < VT; ++h)
-                    if (ty0 + h * TYS == jt) {
-                        const double p = 1.0 / r[h][tri(jb, jb)];
-                        r[h][tri(jb, jb)] = p;
-                        piv = p;
-                        rrow[j] = p;
-                    }
-            }
-            __syncthreads();
-            const double p = piv;
-#pragma unroll
-            for (int h = 0; h < VT; ++h) {
-                const int ty = ty0 + h * TYS;
-                if (ty == jt) {  // row j of the inverse so far, scaled
-#pragma unroll
-                    for (int b = 0; b <= jb; ++b) {
-                        const int c = b * 32 + tx;
-                        if (c < j) {
-                            const double v = r[h][tri(jb, b)] * p;
-                            r[h][tri(jb, b)] = v;
-                            rrow[c] = v;
-                        }
-                    }
-                }
-                if (tx == jt) {  // column j of L below the diagonal (consumed now)
-#pragma unroll
-                    for (int a = jb; a < NB; ++a)
-                        if (a > jb || ty > jt) lcol[a * 32 + ty] = r[h][tri(a, jb)];
-                }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int b = 0; b <= jb; ++b) {
-                const double rc = rrow[b * 32 + tx];
-                const bool colok = (b < jb) || (tx <= jt);
-                const bool cj = (b == jb) && (tx == jt);
-#pragma unroll
-                for (int h = 0; h < VT; ++h) {
-                    const int ty = ty0 + h * TYS;
-#pragma unroll
-                    for (int a = jb; a < NB; ++a) {
-                        const bool rowok = (a > jb) || (ty > jt);  // rows <= j are final
-                        const double old = cj ? 0.0 : r[h][tri(a, b)];
-                        const double upd = fma(-lcol[a * 32 + ty], rc, old);
-                        r[h][tri(a, b)] = (rowok && colok) ? upd : r[h][tri(a, b)];
-                    }
-                }
-            }
-        }
-    }
-    // output: lower part from registers, zeros above
-    for (uint64_t t = tid; t < static_cast<uint64_t>(k) * k; t += NT) {
-        const int i = static_cast<int>(t / k), c = static_cast<int>(t % k);
-        if (c > i) Linv[t] = 0.0f;
-    }
-#pragma unroll
-    for (int h = 0; h < VT; ++h)
-#pragma unroll
-        for (int a = 0; a < NB; ++a)
-#pragma unroll
-            for (int b = 0; b <= a; ++b) {
-                const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
-                if (i < k && c < k && i >= c)
-                    Linv[static_cast<uint64_t>(i) * k + c] = static_cast<float>(r[h][tri(a, b)]);
-            }
-    if (tid == 0 && status) status[0] = attempt;
-}
 
 // Householder tridiagonalisation with the lower triangle in registers.
 // Writes d, e, tau and the reflectors row-wise: H[j][i] = v_j[i] (zero for
@@ -989,29 +836,11 @@ void launch_gram(const float *X, int M, int k, int ld, double *G, double *worksp
     BSQ_HIP(hipGetLastError());
 }
 
-template <int NB>
-static void chol_reg(const double *G, int k, float *Linv, int *status, hipStream_t stream) {
-    constexpr int VT = 1;
-    chol_inv_reg_kernel<NB, VT><<<1, kBig / VT, 0, stream>>>(G, k, Linv, status);
-}
-
+// Unblocked fallback for ranks above the blocked kernel's range (k > 256).
 void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream) {
-    const int nb = static_cast<int>(ceil_div(k, 32));
-    switch (nb) {
-        case 1: chol_reg<1>(G, k, Linv, status, stream); break;
-        case 2: chol_reg<2>(G, k, Linv, status, stream); break;
-        case 3: chol_reg<3>(G, k, Linv, status, stream); break;
-        case 4: chol_reg<4>(G, k, Linv, status, stream); break;
-        case 5: chol_reg<5>(G, k, Linv, status, stream); break;
-        case 6: chol_reg<6>(G, k, Linv, status, stream); break;
-        case 7: chol_reg<7>(G, k, Linv, status, stream); break;
-        case 8: chol_reg<8>(G, k, Linv, status, stream); break;
-        default: {
-            const size_t lds = static_cast<size_t>(k) * sizeof(double);
-            BSQ_REQUIRE(lds <= 64 * 1024, "chol_inv: rank too large");
-            chol_inv_kernel<<<1, kBig, lds, stream>>>(G, k, W, Linv, status);
-        }
-    }
+    const size_t lds = static_cast<size_t>(k) * sizeof(double);
+    BSQ_REQUIRE(lds <= 64 * 1024, "chol_inv: rank too large");
+    chol_inv_kernel<<<1, kBig, lds, stream>>>(G, k, W, Linv, status);
     BSQ_HIP(hipGetLastError());
 }
 
@@ -1049,8 +878,18 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
     BSQ_HIP(hipGetLastError());
     multisect_kernel<<<k, 64, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);
     BSQ_HIP(hipGetLastError());
-    invit_kernel<<<static_cast<unsigned>(ceil_div(k, 64)), 64, 0, stream>>>(d, e, k, lambda, tn, Z, scratch,
-                                                                           iscratch);
+    // eigenvalues per workgroup whose LDS arrays fit: (5kP + 2k) doubles + kP ints
+    const int64_t lds_cap = 160 * 1024;
+    const int P = static_cast<int>(std::min<int64_t>(8, (lds_cap - 16 * static_cast<int64_t>(k)) / (44 * static_cast<int64_t>(k))));
+    if (P >= 1) {
+        const size_t lds = (5 * static_cast<size_t>(k) * P + 2 * k) * sizeof(double) + static_cast<size_t>(k) * P * sizeof(int);
+        BSQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(invit_lds_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        invit_lds_kernel<<<static_cast<unsigned>(ceil_div(k, P)), 64, lds, stream>>>(d, e, k, P, lambda, tn, Z);
+    } else {
+        invit_kernel<<<static_cast<unsigned>(ceil_div(k, 64)), 64, 0, stream>>>(d, e, k, lambda, tn, Z, scratch,
+                                                                               iscratch);
+    }
     BSQ_HIP(hipGetLastError());
     cluster_kernel<<<k, 256, 0, stream>>>(d, e, k, lambda, tn, Z, scratch, iscratch);
     BSQ_HIP(hipGetLastError());

@@ -29,6 +29,9 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
 uint64_t gram_workspace_bytes(int M, int k);
 void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream);
 void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream);
+uint64_t chol_blocked_buffer_doubles(int k);
+bool chol_blocked_supported(int k);
+void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream);
 void launch_syev(const double *G, int k, double *W, double *Z, double *small, double *scratch, int *iscratch,
                  double *lambda, float *Uh, hipStream_t stream);
 
@@ -159,6 +162,7 @@ struct SvdPlan {
     float *R = nullptr, *X = nullptr, *X2 = nullptr, *Y = nullptr, *Y2 = nullptr;
     float *Linv = nullptr, *Uh = nullptr;
     double *G = nullptr, *W = nullptr, *Z = nullptr, *small = nullptr, *scratch = nullptr, *lambda = nullptr;
+    double *Lbuf = nullptr;  // blocked Cholesky: L and the inverses of its diagonal blocks
     int *iscratch = nullptr, *status = nullptr;
     double *gram_ws = nullptr;
     float *gemm_ws = nullptr;
@@ -174,6 +178,7 @@ struct SvdPlan {
         release(Uh);
         release(G);
         release(W);
+        release(Lbuf);
         release(Z);
         release(small);
         release(scratch);
@@ -207,6 +212,7 @@ SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
         p->Uh = alloc<float>(k * k);
         p->G = alloc<double>(k * k);
         p->W = alloc<double>(k * k);
+        if (chol_blocked_supported(static_cast<int>(k))) p->Lbuf = alloc<double>(chol_blocked_buffer_doubles(static_cast<int>(k)));
         p->Z = alloc<double>(k * k);
         p->small = alloc<double>(4 * k + 8);
         p->scratch = alloc<double>(9 * k * k);
@@ -257,7 +263,13 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
     // one CholeskyQR pass: out = in * L^{-T}, G = in^T in = L L^T
     auto orth = [&](const float *in, float *out, int rows) {
         launch_gram(in, rows, k, k, p->G, p->gram_ws, st);
-        launch_chol_inv(p->G, k, p->W, p->Linv, p->status, st);
+        if (p->Lbuf) {  // Linv holds L^{-T}: out = in * Linv
+            launch_chol_blocked(p->G, k, p->Lbuf, p->Linv, p->status, st);
+            launch_gemm(false, false, rows, k, k, in, k, p->Linv, k, out, k, nullptr, nullptr, p->gemm_ws,
+                        p->gemm_ws_bytes, st);
+            return;
+        }
+        launch_chol_inv(p->G, k, p->W, p->Linv, p->status, st);  // Linv holds L^{-1}
         launch_gemm(false, true, rows, k, k, in, k, p->Linv, k, out, k, nullptr, nullptr, p->gemm_ws,
                     p->gemm_ws_bytes, st);
     };
