@@ -37,7 +37,8 @@ NO_CONTRACT = {"quant.hip", "topk.hip", "runtime.hip"}
 # Per-file extra flags: the register-resident FP64 factorisations need their
 # fully unrolled loops kept unrolled so the per-thread matrix stays in VGPRs.
 EXTRA = {"linalg.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
-         "chol.hip": ["-mllvm", "-pragma-unroll-threshold=200000"]}
+         "chol.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
+         "sytrd.hip": ["-mllvm", "-pragma-unroll-threshold=200000"]}
 
 
 def hipcc() -> str:

@@ -287,53 +287,17 @@ __device__ int sturm_count(const double *d, const double *e2, int k, double x, d
     if (fabs(q) < pivmin) q = -pivmin;
     cnt += (q < 0.0);
     for (int i = 1; i < k; ++i) {
-        q = (d[i] - x) - e2[i - 1] / q;
+        // hardware reciprocal + one Newton step (~46 bits) instead of an IEEE
+        // division: only the sign of q is used, and only near an eigenvalue
+        double r = __builtin_amdgcn_rcp(q);
+        r = fma(r, fma(-q, r, 1.0), r);
+        q = fma(-e2[i - 1], r, d[i] - x);
         if (fabs(q) < pivmin) q = -pivmin;
         cnt += (q < 0.0);
     }
     return cnt;
 }
 
-// lambda[t] = t-th largest eigenvalue (bisection to full precision).
-__global__ void bisect_kernel(const double *__restrict__ d, const double *__restrict__ e, int k,
-                              double *__restrict__ lambda, double *__restrict__ e2buf) {
-    extern __shared__ double sm[];  // d[k], e2[k]
-    double *sd = sm, *se2 = sm + k;
-    for (int i = threadIdx.x; i < k; i += blockDim.x) {
-        sd[i] = d[i];
-        se2[i] = (i + 1 < k) ? e[i] * e[i] : 0.0;
-    }
-    __syncthreads();
-    // Gershgorin bounds and pivmin (computed redundantly per workgroup)
-    double lo = 1e300, hi = -1e300, emax = 0.0;
-    for (int i = 0; i < k; ++i) {
-        const double r = (i > 0 ? sqrt(se2[i - 1]) : 0.0) + (i + 1 < k ? sqrt(se2[i]) : 0.0);
-        lo = fmin(lo, sd[i] - r);
-        hi = fmax(hi, sd[i] + r);
-        if (i + 1 < k) emax = fmax(emax, se2[i]);
-    }
-    const double tnorm = fmax(fabs(lo), fabs(hi));
-    const double pivmin = fmax(DBL_MIN, DBL_MIN * emax) * 4.0 + tnorm * 1e-300;
-    lo -= 2.0 * tnorm * DBL_EPSILON * k + pivmin;
-    hi += 2.0 * tnorm * DBL_EPSILON * k + pivmin;
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= k) return;
-    const int target = k - 1 - t;  // ascending index
-    double a = lo, b = hi;
-    for (int it = 0; it < 200; ++it) {
-        const double mid = 0.5 * (a + b);
-        if (mid <= a || mid >= b) break;
-        if (b - a <= 2.0 * DBL_EPSILON * fmax(fabs(a), fabs(b)) + pivmin) break;
-        if (sturm_count(sd, se2, k, mid, pivmin) > target) b = mid;
-        else a = mid;
-    }
-    lambda[t] = 0.5 * (a + b);
-    if (t == 0 && e2buf) e2buf[0] = tnorm;
-}
-
-// LU factorisation with partial pivoting of the tridiagonal T - lam I
-// (LAPACK dlagtf / dlagts in spirit); zero pivots are replaced by `tiny`.
-// Arrays are accessed with a stride so that threads of a wave interleave.
 __device__ void trid_factor(const double *d, const double *e, int k, double lam, double tiny, double *u0,
                             double *u1, double *u2, double *ml, int *piv, int st) {
     double dcur = d[0] - lam, ecur = (k > 1) ? e[0] : 0.0;
@@ -543,169 +507,6 @@ __global__ void backtransform_kernel(const double *__restrict__ W, const double 
     for (int i = lane; i < k; i += 64) Uh[static_cast<uint64_t>(i) * k + t] = static_cast<float>(z[i]);
 }
 
-// ===========================================================================
-// Register-resident versions for k <= 256: the lower triangle of the k x k
-// FP64 matrix lives in the VGPRs of one 1024-thread workgroup, distributed
-// 2-D cyclically: thread (ty, tx) = (tid / 32, tid % 32) owns the elements
-// (a*32 + ty, b*32 + tx), a >= b, of the padded NB*32 matrix.  Every
-// elimination step is one rank-1 (or rank-2) register update plus two LDS
-// broadcasts, so no step touches L2.
-// ===========================================================================
-__device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
-
-// Householder tridiagonalisation with the lower triangle in registers.
-// Writes d, e, tau and the reflectors row-wise: H[j][i] = v_j[i] (zero for
-// i <= j, one at i = j + 1).
-template <int NB, int VT>
-__global__ __launch_bounds__(kBig / VT) void sytrd_reg_kernel(const double *__restrict__ G, int k,
-                                                               double *__restrict__ d, double *__restrict__ e,
-                                                               double *__restrict__ tau, double *__restrict__ H) {
-    constexpr int NE = NB * (NB + 1) / 2;
-    constexpr int KP = NB * 32;
-    constexpr int NT = kBig / VT, TYS = 32 / VT;
-    __shared__ double xs[KP], vs[KP], ws[KP], prow[KP];
-    __shared__ double part[32][KP + 1];
-    __shared__ double red[NT / 64];
-    __shared__ double s_tau;
-    const int tid = threadIdx.x, tx = tid & 31, ty0 = tid >> 5;
-    double r[VT][NE];
-#pragma unroll
-    for (int h = 0; h < VT; ++h)
-#pragma unroll
-        for (int a = 0; a < NB; ++a)
-#pragma unroll
-            for (int b = 0; b <= a; ++b) {
-                const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
-                r[h][tri(a, b)] = (i >= c && i < k && c < k) ? G[static_cast<uint64_t>(i) * k + c] : 0.0;
-            }
-    const int steps = k - 2;  // reflectors j = 0 .. k-3
-#pragma unroll
-    for (int jb = 0; jb < NB; ++jb) {
-        for (int jt = 0; jt < 32; ++jt) {
-            const int j = jb * 32 + jt;
-            if (j >= steps) break;
-            // column j below the diagonal -> xs
-            if (tx == jt) {
-#pragma unroll
-                for (int h = 0; h < VT; ++h) {
-                    const int ty = ty0 + h * TYS;
-#pragma unroll
-                    for (int a = jb; a < NB; ++a)
-                        if (a > jb || ty > jt) xs[a * 32 + ty] = r[h][tri(a, jb)];
-                    if (ty == jt) d[j] = r[h][tri(jb, jb)];
-                }
-            }
-            __syncthreads();
-            // reflector (wave 0): v = [1, x(j+2:) / (alpha - beta)], tau
-            if (tid < 64) {
-                double sig = 0.0;
-                for (int i = j + 2 + tid; i < k; i += 64) sig = fma(xs[i], xs[i], sig);
-                for (int off = 32; off >= 1; off >>= 1) sig += __shfl_xor(sig, off);
-                const double alpha = xs[j + 1];
-                double t = 0.0, beta = alpha, scal = 0.0;
-                if (sig > 0.0) {
-                    const double nrm = sqrt(fma(alpha, alpha, sig));
-                    beta = (alpha >= 0.0) ? -nrm : nrm;
-                    t = (beta - alpha) / beta;
-                    scal = 1.0 / (alpha - beta);
-                }
-                for (int i = tid; i < KP; i += 64) {
-                    double v = 0.0;
-                    if (i == j + 1) v = 1.0;
-                    else if (i > j + 1 && i < k) v = xs[i] * scal;
-                    vs[i] = v;
-                    if (i < k) H[static_cast<uint64_t>(j) * k + i] = v;
-                }
-                if (tid == 0) {
-                    e[j] = beta;
-                    tau[j] = t;
-                    s_tau = t;
-                }
-            }
-            __syncthreads();
-            const double t = s_tau;
-            if (t == 0.0) continue;  // uniform
-            // p = A' v from the lower triangle.  v vanishes at indices <= j,
-            // so stale entries in processed columns contribute nothing to
-            // p[i > j]; p[<= j] is discarded.
-#pragma unroll
-            for (int b = jb; b < NB; ++b) {
-                const double vb = vs[b * 32 + tx];
-#pragma unroll
-                for (int h = 0; h < VT; ++h) {
-                    const int ty = ty0 + h * TYS;
-                    double sc = 0.0;
-#pragma unroll
-                    for (int a = b; a < NB; ++a)
-                        if (a > b || ty > tx) sc = fma(r[h][tri(a, b)], vs[a * 32 + ty], sc);
-                    part[ty][b * 32 + tx] = sc;
-                }
-                (void)vb;
-            }
-#pragma unroll
-            for (int h = 0; h < VT; ++h) {
-                const int ty = ty0 + h * TYS;
-#pragma unroll
-                for (int a = jb; a < NB; ++a) {
-                    double sa = 0.0;
-#pragma unroll
-                    for (int b = jb; b <= a; ++b)
-                        if (a > b || ty >= tx) sa = fma(r[h][tri(a, b)], vs[b * 32 + tx], sa);
-                    for (int off = 16; off >= 1; off >>= 1) sa += __shfl_xor(sa, off, 32);
-                    if (tx == 0) prow[a * 32 + ty] = sa;
-                }
-            }
-            __syncthreads();
-            double pt = 0.0;
-            for (int q = tid; q < KP; q += NT) {
-                if (q > j) {
-                    double s = prow[q];
-                    for (int y = 0; y < 32; ++y) s += part[y][q];
-                    ws[q] = s * t;
-                } else {
-                    ws[q] = 0.0;
-                }
-            }
-            __syncthreads();
-            for (int q = tid; q < KP; q += NT) pt = fma(ws[q], vs[q], pt);
-            const double pv = block_sum(pt, red);
-            for (int q = tid; q < KP; q += NT) ws[q] = (q > j) ? ws[q] - 0.5 * t * pv * vs[q] : 0.0;
-            __syncthreads();
-            // rank-2 update; v and w vanish at indices <= j
-#pragma unroll
-            for (int b = jb; b < NB; ++b) {
-                const double vb = vs[b * 32 + tx], wb = ws[b * 32 + tx];
-#pragma unroll
-                for (int h = 0; h < VT; ++h) {
-                    const int ty = ty0 + h * TYS;
-#pragma unroll
-                    for (int a = b; a < NB; ++a) {
-                        const double va = vs[a * 32 + ty], wa = ws[a * 32 + ty];
-                        r[h][tri(a, b)] = fma(-va, wb, fma(-wa, vb, r[h][tri(a, b)]));
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // trailing 2 x 2 (or 1 x 1) block
-    const int j2 = k - 2;
-#pragma unroll
-    for (int h = 0; h < VT; ++h)
-#pragma unroll
-        for (int a = 0; a < NB; ++a)
-#pragma unroll
-            for (int b = 0; b <= a; ++b) {
-                const int i = a * 32 + ty0 + h * TYS, c = b * 32 + tx;
-                if (i == c && i >= (j2 > 0 ? j2 : 0) && i < k) d[i] = r[h][tri(a, b)];
-                if (j2 >= 0 && i == j2 + 1 && c == j2) e[j2] = r[h][tri(a, b)];
-            }
-    if (tid == 0) {
-        if (k >= 2) tau[k - 2] = 0.0;
-        tau[k - 1] = 0.0;
-    }
-}
-
 // Bisection by multisection: one wave per eigenvalue, 63 interior points per
 // pass.  lambda[t] = t-th largest eigenvalue.
 __global__ __launch_bounds__(64) void multisect_kernel(const double *__restrict__ d, const double *__restrict__ e,
@@ -737,8 +538,11 @@ __global__ __launch_bounds__(64) void multisect_kernel(const double *__restrict_
     const int t = blockIdx.x;
     const int target = k - 1 - t;  // ascending index of the wanted eigenvalue
     double a = lo, b = hi;
+    // absolute tolerance k * eps * ||T|| (a backward-stable eigenvalue is not more
+    // accurate than that): with 64 points per pass that is <= 9 passes
+    const double abstol = static_cast<double>(k) * DBL_EPSILON * tnorm + pivmin;
     for (int pass = 0; pass < 40; ++pass) {
-        if (b - a <= 2.0 * DBL_EPSILON * fmax(fabs(a), fabs(b)) + pivmin) break;
+        if (b - a <= 2.0 * DBL_EPSILON * fmax(fabs(a), fabs(b)) + abstol) break;
         const double h = (b - a) / 64.0;
         const double x = a + h * (lane + 1);  // lanes 0..62 interior, lane 63 = b
         const int cnt = (lane < 63) ? sturm_count(sd, se2, k, x, pivmin) : k + 1;
@@ -810,6 +614,9 @@ __global__ __launch_bounds__(1024) void backtransform_rows_kernel(const double *
 
 }  // namespace
 
+bool sytrd_blocked_supported(int k);
+void launch_sytrd_blocked(const double *G, int k, double *d, double *e, double *tau, double *H, hipStream_t stream);
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -844,12 +651,6 @@ void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status
     BSQ_HIP(hipGetLastError());
 }
 
-template <int NB>
-static void sytrd_reg(const double *G, int k, double *d, double *e, double *tau, double *H, hipStream_t stream) {
-    constexpr int VT = 1;
-    sytrd_reg_kernel<NB, VT><<<1, kBig / VT, 0, stream>>>(G, k, d, e, tau, H);
-}
-
 // Eigen-decomposition of the symmetric G (k x k FP64): lambda descending,
 // Uh[i][t] = component i of eigenvector t (FP32).  `W` k*k doubles, `Z`
 // k*k doubles, `small` >= 4k + 8 doubles, `scratch` 9*k*k doubles,
@@ -858,22 +659,13 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
                  double *lambda, float *Uh, hipStream_t stream) {
     BSQ_REQUIRE(k >= 1 && static_cast<size_t>(2 * k) * sizeof(double) <= 64 * 1024, "syev: rank too large");
     double *d = small, *e = small + k, *tau = small + 2 * k, *tn = small + 3 * k;
-    const int nb = static_cast<int>(ceil_div(k, 32));
     bool reg = true;
-    switch (nb) {
-        case 1: sytrd_reg<1>(G, k, d, e, tau, W, stream); break;
-        case 2: sytrd_reg<2>(G, k, d, e, tau, W, stream); break;
-        case 3: sytrd_reg<3>(G, k, d, e, tau, W, stream); break;
-        case 4: sytrd_reg<4>(G, k, d, e, tau, W, stream); break;
-        case 5: sytrd_reg<5>(G, k, d, e, tau, W, stream); break;
-        case 6: sytrd_reg<6>(G, k, d, e, tau, W, stream); break;
-        case 7: sytrd_reg<7>(G, k, d, e, tau, W, stream); break;
-        case 8: sytrd_reg<8>(G, k, d, e, tau, W, stream); break;
-        default:
-            reg = false;
-            BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice,
-                                   stream));
-            sytrd_kernel<<<1, kBig, 2 * k * sizeof(double), stream>>>(W, k, d, e, tau);
+    if (sytrd_blocked_supported(k)) {
+        launch_sytrd_blocked(G, k, d, e, tau, W, stream);
+    } else {
+        reg = false;
+        BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));
+        sytrd_kernel<<<1, kBig, 2 * k * sizeof(double), stream>>>(W, k, d, e, tau);
     }
     BSQ_HIP(hipGetLastError());
     multisect_kernel<<<k, 64, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);

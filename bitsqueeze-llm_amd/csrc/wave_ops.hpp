@@ -1,0 +1,41 @@
+// Cross-lane reductions for one 64-lane wave through DPP lane moves (VALU
+// operations; no LDS round trip, unlike __shfl_*).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace bsq {
+
+// v of the lane selected by the DPP control CTRL; lanes of rows outside
+// ROW_MASK (and lanes whose source is out of range) read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_read(double v) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(u & 0xffffffffu), CTRL, ROW_MASK, 0xF, false));
+    const unsigned hi = static_cast<unsigned>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, ROW_MASK, 0xF, false));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// sum over each aligned group of 4 lanes, in every lane of the group
+__device__ __forceinline__ double quad_sum(double v) {
+    v += dpp_read<0xB1>(v);  // quad_perm [1, 0, 3, 2]
+    v += dpp_read<0x4E>(v);  // quad_perm [2, 3, 0, 1]
+    return v;
+}
+
+// sum over all 64 lanes (every lane must be active), returned to every lane
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+    v = quad_sum(v);
+    v += dpp_read<0x141>(v);       // row_half_mirror: 8-lane sums
+    v += dpp_read<0x140>(v);       // row_mirror: 16-lane row sums
+    v += dpp_read<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+    v += dpp_read<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3: lane 63 holds the total
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), 63));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), 63));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+}  // namespace bsq
