@@ -16,6 +16,7 @@
 // so that the error-correction pass never materialises the error matrix.
 #include "bsq_internal.hpp"
 
+#include <algorithm>
 #include <cfloat>
 
 namespace bsq {
@@ -80,8 +81,17 @@ struct Shared {
     uint32_t wsum[kThreads / 64];
     uint32_t digit, above;  // chosen digit, count strictly above it
     uint32_t ncand;
+    unsigned long long kt, kth;  // filter threshold, k-th largest composite key (fast path)
     float L[16];
 };
+
+// Fast path (row cached, k <= 256): at most this many candidates are ranked
+// directly; more fall back to the radix select.
+constexpr uint32_t kFastCap = 512;
+
+__device__ __forceinline__ unsigned long long composite_key(float v, uint32_t c) {
+    return (static_cast<unsigned long long>(order_key(v)) << 16) | (0xFFFFu - c);
+}
 
 // One radix pass: histogram of digit (K >> shift) & 255 over entries whose
 // already-decided high part equals `prefix`, then choose the digit holding
@@ -119,7 +129,11 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
         sh.L[threadIdx.x] = Lc[threadIdx.x];
     }
     for (uint32_t w = threadIdx.x; w < nwords; w += kThreads) selbits[w] = 0;
-    if (threadIdx.x == 0) sh.ncand = 0;
+    if (threadIdx.x == 0) {
+        sh.ncand = 0;
+        sh.kt = 0;
+        sh.kth = 0;
+    }
     float dq = 1.0f;
     if constexpr (SRC == TopkSource::DenseMinusNF4DQ) {
         dq = *a.dq;
@@ -135,11 +149,34 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
     // Phase 0: values of the row (into LDS when cached) and the any-nonzero
     // test of device_buffer_has_nonzero (src/bitsqz_llm.cu:175-184, 396-423).
     bool nonzero = false;
+    unsigned long long tmax = 0;  // largest composite key among this thread's columns
+    const bool vec4 = ((cols & 3u) == 0) && ((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0);
     if constexpr (CACHED) {
-        for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
-            const float v = load_value<SRC>(a, sh.L, dq, row0 + c);
-            cache[c] = v;
-            nonzero |= fabsf(v) > FLT_EPSILON;
+        if (SRC == TopkSource::Dense && vec4) {
+            // 16-byte loads, several in flight per lane: the row is read once
+            const float4 *src4 = reinterpret_cast<const float4 *>(a.a + row0);
+            float4 *cache4 = reinterpret_cast<float4 *>(cache);
+#pragma unroll 4
+            for (uint32_t c4 = threadIdx.x; c4 < cols / 4; c4 += kThreads) {
+                const float4 v4 = src4[c4];
+                cache4[c4] = v4;
+                const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    nonzero |= fabsf(vv[u]) > FLT_EPSILON;
+                    const unsigned long long K = composite_key(vv[u], 4 * c4 + u);
+                    tmax = K > tmax ? K : tmax;
+                }
+            }
+        } else {
+#pragma unroll 4
+            for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
+                const float v = load_value<SRC>(a, sh.L, dq, row0 + c);
+                cache[c] = v;
+                nonzero |= fabsf(v) > FLT_EPSILON;
+                const unsigned long long K = composite_key(v, c);
+                tmax = K > tmax ? K : tmax;
+            }
         }
     } else if (a.flags) {
         for (uint32_t c = threadIdx.x; c < cols; c += kThreads)
@@ -149,6 +186,82 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
         if (threadIdx.x == 0) atomicOr(a.flags, kFlagError);
     }
     __syncthreads();
+
+    uint16_t *out_idx = a.indices + static_cast<uint64_t>(r) * k;
+    float *out_val = a.values + static_cast<uint64_t>(r) * k;
+    if constexpr (CACHED) {
+        // the filter needs at least k non-empty lanes (lanes own 4 columns
+        // each on the 16-byte path, 1 otherwise)
+        const uint32_t groups = (SRC == TopkSource::Dense && vec4) ? cols / 4 : cols;
+        if (k <= kThreads && k <= groups) {
+            // Filter: the k-th largest of the per-thread maxima is a key that at
+            // least k entries reach, and few more than k do for any spread-out
+            // row.  Rank the entries at or above it directly (keys are unique);
+            // fall back to the radix select when there are too many.
+            unsigned long long *tm = reinterpret_cast<unsigned long long *>(dyn + cache_bytes);
+            unsigned long long *buf = tm + kThreads;
+            tm[threadIdx.x] = tmax;
+            __syncthreads();
+            uint32_t above = 0;
+            for (uint32_t j = 0; j < kThreads; ++j) above += (tm[j] > tmax) ? 1u : 0u;
+            if (above == k - 1) sh.kt = tmax;  // one thread: the maxima of non-empty threads are distinct
+            __syncthreads();
+            const unsigned long long kt = sh.kt;
+            uint32_t cnt = 0;
+            for (uint32_t c = threadIdx.x; c < cols; c += kThreads) cnt += (composite_key(cache[c], c) >= kt) ? 1u : 0u;
+            const uint32_t incl = block_inclusive_scan(cnt, sh.wsum);
+            if (threadIdx.x == kThreads - 1) sh.ncand = incl;
+            __syncthreads();
+            const uint32_t total = sh.ncand;
+            if (total <= kFastCap) {
+                uint32_t pos = incl - cnt;
+                for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
+                    const unsigned long long K = composite_key(cache[c], c);
+                    if (K >= kt) buf[pos++] = K;
+                }
+                __syncthreads();
+                for (uint32_t i = threadIdx.x; i < total; i += kThreads) {
+                    const unsigned long long mine = buf[i];
+                    uint32_t rank = 0;
+                    for (uint32_t j = 0; j < total; ++j) rank += (buf[j] > mine) ? 1u : 0u;
+                    if (rank < k) {
+                        const uint32_t col = 0xFFFFu - static_cast<uint32_t>(mine & 0xFFFFu);
+                        out_idx[rank] = static_cast<uint16_t>(col);
+                        out_val[rank] = cache[col];
+                        if (rank == k - 1) sh.kth = mine;
+                    }
+                }
+                if (a.residual) {
+                    __syncthreads();
+                    const unsigned long long kth = sh.kth;
+                    float *res = a.residual + row0;
+                    if ((cols & 3u) == 0 && (reinterpret_cast<uintptr_t>(a.residual) & 15u) == 0) {
+                        const float4 *cache4 = reinterpret_cast<const float4 *>(cache);
+#pragma unroll 4
+                        for (uint32_t c4 = threadIdx.x; c4 < cols / 4; c4 += kThreads) {
+                            float4 v = cache4[c4];
+                            const uint32_t c = 4 * c4;
+                            v.x = (composite_key(v.x, c + 0) >= kth) ? 0.0f : v.x;
+                            v.y = (composite_key(v.y, c + 1) >= kth) ? 0.0f : v.y;
+                            v.z = (composite_key(v.z, c + 2) >= kth) ? 0.0f : v.z;
+                            v.w = (composite_key(v.w, c + 3) >= kth) ? 0.0f : v.w;
+                            reinterpret_cast<float4 *>(res)[c4] = v;
+                        }
+                    } else {
+                        for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
+                            const float v = cache[c];
+                            res[c] = (composite_key(v, c) >= kth) ? 0.0f : v;
+                        }
+                    }
+                }
+                return;  // uniform
+            }
+            __syncthreads();  // the radix path below reuses this LDS
+            for (uint32_t w = threadIdx.x; w < nwords; w += kThreads) selbits[w] = 0;
+            if (threadIdx.x == 0) sh.ncand = 0;
+            __syncthreads();
+        }
+    }
 
     // Phase 1: radix select on the 32-bit key, then (if the threshold key is
     // shared by more entries than still needed) on the inverted column.
@@ -212,8 +325,6 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
     __syncthreads();
 
     // Phase 3: order the k entries by K descending.
-    uint16_t *out_idx = a.indices + static_cast<uint64_t>(r) * k;
-    float *out_val = a.values + static_cast<uint64_t>(r) * k;
     if (k <= kThreads) {
         // rank sort: each thread places one entry
         if (threadIdx.x < k) {
@@ -263,6 +374,233 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
     }
 }
 
+// Register-resident variant for rows of up to 4096 columns with cols % 4 == 0
+// and k <= 256: each lane keeps its NV4 column quads of the row in
+// VGPRs (lane t owns columns 4 (t + 256 m) .. + 3), so LDS holds only the
+// small selection arrays and many rows run per CU.  Selection as in the
+// cached kernel's filter path (k-th largest lane maximum, then ranking of
+// the entries at or above it), with the radix select over the registers as
+// the fallback when the filter keeps more than kFastCap entries.
+template <TopkSource SRC, int NV4>
+__global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
+    __shared__ Shared sh;
+    __shared__ unsigned long long tm[kThreads];
+    __shared__ unsigned long long bk[kFastCap];
+    __shared__ float bv[kFastCap];
+    const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
+    const uint32_t r = blockIdx.x, tid = threadIdx.x;
+    const uint64_t row0 = static_cast<uint64_t>(r) * cols;
+    if (tid < 16) {
+        constexpr float Lc[16] = BSQ_NF4_LEVELS;
+        sh.L[tid] = Lc[tid];
+    }
+    if (tid == 0) {
+        sh.kt = 0;
+        sh.kth = 0;
+        sh.ncand = 0;
+    }
+    float dq = 1.0f;
+    if constexpr (SRC == TopkSource::DenseMinusNF4DQ) {
+        dq = *a.dq;
+        if (dq == 0.0f || !__builtin_isfinite(dq)) dq = 1.0f;
+    }
+    __syncthreads();
+
+    // the row: v[m][u] = column 4 (tid + 256 m) + u.  Absent columns (>= cols)
+    // hold NaN: their composite keys are below every real entry's (NaN key 0,
+    // and a smaller inverted column than any real NaN), so they never reach
+    // the selection and need no bound checks.
+    float v[NV4][4];
+#pragma unroll
+    for (int m = 0; m < NV4; ++m) {
+        const uint32_t c4 = tid + kThreads * m;
+        if (c4 < q4) {
+            if constexpr (SRC == TopkSource::Dense) {
+                const float4 x = reinterpret_cast<const float4 *>(a.a + row0)[c4];
+                v[m][0] = x.x;
+                v[m][1] = x.y;
+                v[m][2] = x.z;
+                v[m][3] = x.w;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[m][u] = load_value<SRC>(a, sh.L, dq, row0 + 4 * c4 + u);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[m][u] = __builtin_nanf("");
+        }
+    }
+    // keys are recomputed from the values in every phase (an opaque copy of
+    // the lane index stops the compiler from keeping 2 * 4 * NV4 key registers
+    // live across the phases)
+    auto key_of = [&](uint32_t t, int m, int u) -> unsigned long long {
+        return composite_key(v[m][u], 4 * (t + kThreads * m) + u);
+    };
+    auto lane_id = [&]() -> uint32_t {
+        uint32_t t = threadIdx.x;
+        asm volatile("" : "+v"(t));
+        return t;
+    };
+    bool nonzero = false;
+    unsigned long long tmax = 0;
+    uint32_t lt = lane_id();
+#pragma unroll
+    for (int m = 0; m < NV4; ++m) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            nonzero |= fabsf(v[m][u]) > FLT_EPSILON;  // false for the NaN padding
+            const unsigned long long K = key_of(lt, m, u);
+            tmax = K > tmax ? K : tmax;
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep each quad's keys short-lived
+    }
+    if (a.flags && __syncthreads_or(nonzero ? 1 : 0)) {
+        if (tid == 0) atomicOr(a.flags, kFlagError);
+    }
+    tm[tid] = tmax;
+    __syncthreads();
+    uint32_t above = 0;
+    for (uint32_t j = 0; j < kThreads; ++j) above += (tm[j] > tmax) ? 1u : 0u;
+    if (above == k - 1) sh.kt = tmax;  // lanes with columns have distinct maxima; k <= those lanes
+    __syncthreads();
+    unsigned long long kt = sh.kt;
+    uint32_t cnt = 0;
+    lt = lane_id();
+#pragma unroll
+    for (int m = 0; m < NV4; ++m) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) cnt += (key_of(lt, m, u) >= kt) ? 1u : 0u;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    uint32_t incl = block_inclusive_scan(cnt, sh.wsum);
+    if (tid == kThreads - 1) sh.ncand = incl;
+    __syncthreads();
+    uint32_t total = sh.ncand;
+    if (total > kFastCap) {
+        // fallback: exact threshold by radix select over the registers, on the
+        // 32-bit key, then on the inverted column among equal keys
+        uint32_t prefix = 0, mask = 0, remaining = k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            sh.hist[tid] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < NV4; ++m)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t key = order_key(v[m][u]);
+                    if ((key & mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            __syncthreads();
+            choose_digit(sh, remaining);
+            prefix |= sh.digit << shift;
+            mask |= 255u << shift;
+            remaining -= sh.above;
+            __syncthreads();
+        }
+        const uint32_t tkey = prefix;
+        uint32_t cpre = 0, cmask = 0;
+        for (int shift = 8; shift >= 0; shift -= 8) {
+            sh.hist[tid] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < NV4; ++m)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t inv = 0xFFFFu - (4 * (tid + kThreads * m) + u);
+                    if (order_key(v[m][u]) == tkey && (inv & cmask) == cpre)
+                        atomicAdd(&sh.hist[(inv >> shift) & 255u], 1u);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            __syncthreads();
+            choose_digit(sh, remaining);
+            cpre |= sh.digit << shift;
+            cmask |= 255u << shift;
+            remaining -= sh.above;
+            __syncthreads();
+        }
+        kt = (static_cast<unsigned long long>(tkey) << 16) | cpre;  // exactly k keys are >= kt
+        cnt = 0;
+        lt = lane_id();
+#pragma unroll
+        for (int m = 0; m < NV4; ++m) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) cnt += (key_of(lt, m, u) >= kt) ? 1u : 0u;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        incl = block_inclusive_scan(cnt, sh.wsum);
+        total = k;
+    }
+    // collect the entries at or above kt with their values, then rank them
+    uint32_t pos = incl - cnt;
+    lt = lane_id();
+#pragma unroll
+    for (int m = 0; m < NV4; ++m) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const unsigned long long K = key_of(lt, m, u);
+            if (K >= kt) {
+                bk[pos] = K;
+                bv[pos] = v[m][u];
+                ++pos;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+    uint16_t *out_idx = a.indices + static_cast<uint64_t>(r) * k;
+    float *out_val = a.values + static_cast<uint64_t>(r) * k;
+    for (uint32_t i = tid; i < total; i += kThreads) {
+        const unsigned long long mine = bk[i];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < total; ++j) rank += (bk[j] > mine) ? 1u : 0u;
+        if (rank < k) {
+            out_idx[rank] = static_cast<uint16_t>(0xFFFFu - static_cast<uint32_t>(mine & 0xFFFFu));
+            out_val[rank] = bv[i];
+            if (rank == k - 1) sh.kth = mine;
+        }
+    }
+    if (a.residual) {
+        __syncthreads();
+        const unsigned long long kth = sh.kth;
+        float4 *res4 = reinterpret_cast<float4 *>(a.residual + row0);
+        lt = lane_id();
+#pragma unroll
+        for (int m = 0; m < NV4; ++m) {
+            const uint32_t c4 = lt + kThreads * m;
+            if (c4 < q4) {
+                float4 o;
+                o.x = (key_of(lt, m, 0) >= kth) ? 0.0f : v[m][0];
+                o.y = (key_of(lt, m, 1) >= kth) ? 0.0f : v[m][1];
+                o.z = (key_of(lt, m, 2) >= kth) ? 0.0f : v[m][2];
+                o.w = (key_of(lt, m, 3) >= kth) ? 0.0f : v[m][3];
+                res4[c4] = o;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+template <TopkSource SRC, int NV4>
+void launch_reg(const TopkArgs &a, hipStream_t stream) {
+    topk_reg_kernel<SRC, NV4><<<a.rows, kThreads, 0, stream>>>(a);
+}
+
+// True (and launched) when the register-resident kernel serves this shape.
+template <TopkSource SRC>
+bool try_launch_reg(const TopkArgs &a, hipStream_t stream) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a.a) | reinterpret_cast<uintptr_t>(a.residual) |
+                         (SRC == TopkSource::DenseMinusDense ? reinterpret_cast<uintptr_t>(a.b) : 0);
+    if ((a.cols & 3u) != 0 || (al & 15u) != 0 || a.k > kThreads || a.k > a.cols / 4) return false;
+    // longer rows need more than 128 VGPRs per lane here, which halves the
+    // resident rows; the LDS-cached kernel serves them better
+    const uint32_t nv4 = static_cast<uint32_t>(ceil_div(a.cols / 4, kThreads));
+    if (nv4 <= 2) launch_reg<SRC, 2>(a, stream);
+    else if (nv4 <= 4) launch_reg<SRC, 4>(a, stream);
+    else return false;
+    return true;
+}
+
 __global__ void topk_scatter_kernel(const uint16_t *__restrict__ idx0, const float *__restrict__ val0, uint32_t k0,
                                     const uint16_t *__restrict__ idx1, const float *__restrict__ val1, uint32_t k1,
                                     uint32_t cols, float *__restrict__ dense, bool accumulate,
@@ -287,11 +625,13 @@ __global__ void topk_scatter_kernel(const uint16_t *__restrict__ idx0, const flo
 
 template <TopkSource SRC>
 void launch_src(const TopkArgs &a, hipStream_t stream) {
+    if (try_launch_reg<SRC>(a, stream)) return;
     uint32_t P = 1;
     while (P < a.k) P <<= 1;
     const bool cached = a.cols <= kCacheMaxCols;
     const size_t cache_bytes = cached ? ((a.cols * 4u + 15u) & ~15u) : 0u;
-    const size_t lds = cache_bytes + static_cast<size_t>(P) * 8 + ((a.cols + 31) / 32) * 4;
+    size_t lds = cache_bytes + static_cast<size_t>(P) * 8 + ((a.cols + 31) / 32) * 4;
+    if (cached && a.k <= kThreads) lds = std::max(lds, cache_bytes + static_cast<size_t>(kThreads + kFastCap) * 8);
     BSQ_REQUIRE(lds + sizeof(Shared) <= 160u * 1024u, "top-k: row too large for the LDS sort");
     if (cached) {
         auto kern = topk_select_kernel<SRC, true>;

@@ -82,3 +82,22 @@ def test_separation_in_place_large():
     expect = x.copy()
     np.put_along_axis(expect, ei.astype(np.int64), 0.0, axis=1)
     assert res.tobytes() == expect.tobytes()
+
+
+@pytest.mark.parametrize("k", [16, 110, 256])
+def test_filter_fallback_and_separation(k):
+    """Rows whose largest entries all fall on the same 256-column residues
+    (column % 256 < k) defeat the per-thread-maximum filter (about 43 k
+    candidates), so the radix select takes over; other rows in the same launch
+    take the filter path.  Both must give the oracle's bytes, including the
+    separation residual."""
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((8, 11008)).astype(np.float32)
+    big = (np.arange(11008) % 256) < k
+    x[::2, big] = (rng.standard_normal(int(big.sum())) * 100.0).astype(np.float32)  # even rows: fallback
+    idx, val, res = B.topk_select(x, k, separate=True)
+    ei, ev = O.topk_rows(x, k)
+    assert idx.tobytes() == ei.tobytes() and val.tobytes() == ev.tobytes()
+    expect = x.copy()
+    np.put_along_axis(expect, ei.astype(np.int64), 0.0, axis=1)
+    assert res.tobytes() == expect.tobytes()
