@@ -194,30 +194,71 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
         // each on the 16-byte path, 1 otherwise)
         const uint32_t groups = (SRC == TopkSource::Dense && vec4) ? cols / 4 : cols;
         if (k <= kThreads && k <= groups) {
-            // Filter: the k-th largest of the per-thread maxima is a key that at
-            // least k entries reach, and few more than k do for any spread-out
-            // row.  Rank the entries at or above it directly (keys are unique);
-            // fall back to the radix select when there are too many.
+            // Filter: the k-th largest of the lane (or lane-pair) maxima is a key
+            // that at least k entries reach, and few more than k do for any
+            // spread-out row.  Rank the entries at or above it directly (keys are
+            // unique); fall back to the radix select when there are too many.
             unsigned long long *tm = reinterpret_cast<unsigned long long *>(dyn + cache_bytes);
             unsigned long long *buf = tm + kThreads;
-            tm[threadIdx.x] = tmax;
+            // pairs of lanes when k allows: half the maxima to rank against
+            const uint32_t nonempty = min(kThreads, groups);
+            const bool pairs = 2 * k <= nonempty + 1 && k <= kThreads / 2;
+            unsigned long long gmax = tmax;
+            if (pairs) {
+                const unsigned long long other = static_cast<unsigned long long>(static_cast<uint32_t>(
+                    __builtin_amdgcn_update_dpp(0, static_cast<int>(tmax & 0xffffffffu), 0xB1, 0xF, 0xF, false))) |
+                    (static_cast<unsigned long long>(static_cast<uint32_t>(
+                        __builtin_amdgcn_update_dpp(0, static_cast<int>(tmax >> 32), 0xB1, 0xF, 0xF, false))) << 32);
+                gmax = other > tmax ? other : tmax;
+                if ((threadIdx.x & 1u) == 0) tm[threadIdx.x >> 1] = gmax;
+            } else {
+                tm[threadIdx.x] = tmax;
+            }
+            const uint32_t ng = pairs ? kThreads / 2 : kThreads;
             __syncthreads();
             uint32_t above = 0;
-            for (uint32_t j = 0; j < kThreads; ++j) above += (tm[j] > tmax) ? 1u : 0u;
-            if (above == k - 1) sh.kt = tmax;  // one thread: the maxima of non-empty threads are distinct
+            const ulonglong2 *tm2 = reinterpret_cast<const ulonglong2 *>(tm);
+            for (uint32_t j = 0; j < ng / 2; ++j) {
+                const ulonglong2 t2 = tm2[j];
+                above += (t2.x > gmax ? 1u : 0u) + (t2.y > gmax ? 1u : 0u);
+            }
+            // one group ranks k-1: the maxima of non-empty groups are distinct
+            if (above == k - 1 && (!pairs || (threadIdx.x & 1u) == 0)) sh.kt = gmax;
             __syncthreads();
             const unsigned long long kt = sh.kt;
+            // count with a bitmask of this lane's hits (<= 64 entries per lane)
+            unsigned long long hits = 0;
             uint32_t cnt = 0;
-            for (uint32_t c = threadIdx.x; c < cols; c += kThreads) cnt += (composite_key(cache[c], c) >= kt) ? 1u : 0u;
+            const bool quads = (cols & 3u) == 0;
+            if (quads) {
+                const float4 *cache4 = reinterpret_cast<const float4 *>(cache);
+                uint32_t i = 0;
+#pragma unroll 4
+                for (uint32_t c4 = threadIdx.x; c4 < cols / 4; c4 += kThreads, ++i) {
+                    const float4 q = cache4[c4];
+                    const uint32_t c = 4 * c4;
+                    const unsigned long long b0 = composite_key(q.x, c) >= kt, b1 = composite_key(q.y, c + 1) >= kt,
+                                             b2 = composite_key(q.z, c + 2) >= kt, b3 = composite_key(q.w, c + 3) >= kt;
+                    hits |= (b0 | (b1 << 1) | (b2 << 2) | (b3 << 3)) << (4 * i);
+                }
+            } else {
+                uint32_t i = 0;
+                for (uint32_t c = threadIdx.x; c < cols; c += kThreads, ++i)
+                    hits |= static_cast<unsigned long long>(composite_key(cache[c], c) >= kt) << i;
+            }
+            cnt = static_cast<uint32_t>(__popcll(hits));
             const uint32_t incl = block_inclusive_scan(cnt, sh.wsum);
             if (threadIdx.x == kThreads - 1) sh.ncand = incl;
             __syncthreads();
             const uint32_t total = sh.ncand;
             if (total <= kFastCap) {
                 uint32_t pos = incl - cnt;
-                for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
-                    const unsigned long long K = composite_key(cache[c], c);
-                    if (K >= kt) buf[pos++] = K;
+                while (hits) {
+                    const uint32_t b = static_cast<uint32_t>(__ffsll(static_cast<long long>(hits)) - 1);
+                    hits &= hits - 1;
+                    const uint32_t c = quads ? 4 * (threadIdx.x + kThreads * (b >> 2)) + (b & 3u)
+                                             : threadIdx.x + kThreads * b;
+                    buf[pos++] = composite_key(cache[c], c);
                 }
                 __syncthreads();
                 for (uint32_t i = threadIdx.x; i < total; i += kThreads) {
