@@ -15,8 +15,8 @@
 // Tiling: 256 threads = 4 waves in a 2 x 2 grid; workgroup tile 128 x 128,
 // BK = 32; each wave owns 64 x 64 as 4 x 4 MFMA 16x16 blocks (64 AGPRs).
 // Tiles move global -> registers (16-byte loads where the layout allows)
-// -> LDS (k-major, padded, so every MFMA operand read is 16 consecutive
-// floats) while the previous tile is multiplied.  Skinny shapes are split
+// -> LDS in their global orientation (16-byte writes; layouts below) while
+// the previous tile is multiplied.  Skinny shapes are split
 // along K so the grid fills the 256 CUs several times over; partial products
 // go to a workspace summed in a fixed order, so results are deterministic.
 #include "bsq_internal.hpp"
@@ -28,7 +28,6 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int PAD = 16;  // row stride = 16 mod 64 banks: MFMA operand reads conflict-free
 
 struct GemmArgs {
     const float *A;
@@ -43,21 +42,32 @@ struct GemmArgs {
     bool vec_a, vec_b;        // 16-byte loads allowed (alignment of base and leading dim)
 };
 
-// A "row-contiguous" operand tile: R rows x 32 k-values, k contiguous in
-// memory (A for TA = false, B for TB = true).  Written to LDS transposed as
-// S[k][row].  256 threads: thread t covers row (t % 128) + 128 * pass, k
-// quad (t / 128) * 4 + 8 * q.
+// LDS tile layouts.  The 16x16x4 MFMA takes, in lane l = 16 kk + i, the
+// operand element (row / column i, k), and the k order inside a BK slice is
+// free as long as both operands use the same one.  Lane kk takes
+// k = 8 kk + s at MFMA step s (s = 0..7), so:
+//   k-contiguous tiles (A with TA = false, B with TB = true) are kept as
+//   [row][k] (pitch 36 floats): a lane's 8 k-values of a fragment are two
+//   16-byte reads, and the rows of 16 lanes start 36 banks apart (no
+//   conflicts); the global tile is stored as loaded (16-byte LDS writes);
+//   k-major tiles (A with TA = true, B with TB = false) are kept as [k][col]
+//   (pitch R + 4): one 4-byte read per step, 16-byte LDS writes.
+constexpr int PK = BK + 4;
+
+// k-contiguous operand tile: R rows x 32 k-values.  256 threads: thread t
+// covers row (t % R) + R * pass, k quad (t / R) ... (8 quads per row).
 template <int R>
 struct KContig {
     static constexpr int N4 = R * BK / 4 / kThreads;  // float4 per thread
+    using Tile = float[R][PK];
     float4 v[N4];
     __device__ __forceinline__ void load(const float *__restrict__ P, int ld, int r0, int rows, int k0, int kend,
                                          bool vec, const float *__restrict__ colscale) {
         const int t = threadIdx.x;
 #pragma unroll
         for (int q = 0; q < N4; ++q) {
-            const int lin = t + q * kThreads;       // 0 .. R*8-1
-            const int r = lin % R, kq = lin / R;    // kq in 0..7
+            const int lin = t + q * kThreads;  // 0 .. R*8-1
+            const int r = lin % R, kq = lin / R;
             const int gr = r0 + r, gk = k0 + kq * 4;
             float4 x;
             if (vec && gr < rows && gk + 4 <= kend) {
@@ -78,26 +88,34 @@ struct KContig {
             v[q] = x;
         }
     }
-    template <int LDW>
-    __device__ __forceinline__ void store(float (*S)[LDW]) const {
+    __device__ __forceinline__ void store(Tile &S) const {
         const int t = threadIdx.x;
 #pragma unroll
         for (int q = 0; q < N4; ++q) {
             const int lin = t + q * kThreads;
-            const int r = lin % R, kq = lin / R;
-            S[kq * 4 + 0][r] = v[q].x;
-            S[kq * 4 + 1][r] = v[q].y;
-            S[kq * 4 + 2][r] = v[q].z;
-            S[kq * 4 + 3][r] = v[q].w;
+            *reinterpret_cast<float4 *>(&S[lin % R][(lin / R) * 4]) = v[q];
         }
+    }
+    // the 8 k-values (k = 8 kk + s) of row `row` for this lane
+    __device__ __forceinline__ static void frag(const Tile &S, int row, int kk, float (&o)[8]) {
+        const float4 lo = *reinterpret_cast<const float4 *>(&S[row][8 * kk]);
+        const float4 hi = *reinterpret_cast<const float4 *>(&S[row][8 * kk + 4]);
+        o[0] = lo.x;
+        o[1] = lo.y;
+        o[2] = lo.z;
+        o[3] = lo.w;
+        o[4] = hi.x;
+        o[5] = hi.y;
+        o[6] = hi.z;
+        o[7] = hi.w;
     }
 };
 
-// A "k-major" operand tile: 32 k-rows x C contiguous values (A for TA = true,
-// B for TB = false).  Written to LDS as S[k][c].
+// k-major operand tile: 32 k-rows x Cn contiguous values.
 template <int Cn>
 struct KMajor {
     static constexpr int N4 = Cn * BK / 4 / kThreads;
+    using Tile = float[BK][Cn + 4];
     float4 v[N4];
     __device__ __forceinline__ void load(const float *__restrict__ P, int ld, int c0, int cols, int k0, int kend,
                                          bool vec, const float *__restrict__ rowscale) {
@@ -119,25 +137,27 @@ struct KMajor {
                 x.w = (gk < kend && gc + 3 < cols) ? row[gc + 3] : 0.0f;
             }
             if (rowscale) {
-                const float s = (gk < kend) ? rowscale[gk] : 0.0f;
-                x.x *= s;
-                x.y *= s;
-                x.z *= s;
-                x.w *= s;
+                const float sc = (gk < kend) ? rowscale[gk] : 0.0f;
+                x.x *= sc;
+                x.y *= sc;
+                x.z *= sc;
+                x.w *= sc;
             }
             v[q] = x;
         }
     }
-    template <int LDW>
-    __device__ __forceinline__ void store(float (*S)[LDW]) const {
+    __device__ __forceinline__ void store(Tile &S) const {
         const int t = threadIdx.x;
         constexpr int C4 = Cn / 4;
 #pragma unroll
         for (int q = 0; q < N4; ++q) {
             const int lin = t + q * kThreads;
-            const int c = (lin % C4) * 4, kk = lin / C4;
-            *reinterpret_cast<float4 *>(&S[kk][c]) = v[q];
+            *reinterpret_cast<float4 *>(&S[lin / C4][(lin % C4) * 4]) = v[q];
         }
+    }
+    __device__ __forceinline__ static void frag(const Tile &S, int col, int kk, float (&o)[8]) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) o[s] = S[8 * kk + s][col];
     }
 };
 
@@ -148,8 +168,16 @@ template <bool TA, bool TB, bool RECON>
 __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
     constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
     constexpr int FM = WM / 16, FN = WN / 16;
-    __shared__ __attribute__((aligned(16))) float As[2][BK][BM + PAD];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK][BN + PAD];
+    using TileA = typename std::conditional<TA, KMajor<BM>, KContig<BM>>::type;
+    using TileB = typename std::conditional<TB, KContig<BN>, KMajor<BN>>::type;
+    // one LDS block: the double-buffered operand tiles, reused by the
+    // reconstruction epilogue to stage the output tile
+    constexpr size_t kABytes = 2 * sizeof(typename TileA::Tile), kBBytes = 2 * sizeof(typename TileB::Tile);
+    constexpr size_t kCBytes = RECON ? sizeof(float) * BM * (BN + 4) : 0;
+    constexpr size_t kSmem = (kABytes + kBBytes > kCBytes) ? kABytes + kBBytes : kCBytes;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
+    typename TileA::Tile *As = reinterpret_cast<typename TileA::Tile *>(smem);
+    typename TileB::Tile *Bs = reinterpret_cast<typename TileB::Tile *>(smem + kABytes);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
@@ -163,11 +191,10 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
-    typename std::conditional<TA, KMajor<BM>, KContig<BM>>::type ta;
-    typename std::conditional<TB, KContig<BN>, KMajor<BN>>::type tb;
-
+    TileA ta;
+    TileB tb;
     auto load = [&](int k0) {
-        ta.load(g.A, g.lda, m0, g.M, k0, kend, g.vec_a, RECON ? g.a_colscale : nullptr);
+        ta.load(g.A, g.lda, m0, g.M, k0, kend, g.vec_a, nullptr);
         tb.load(g.B, g.ldb, n0, g.N, k0, kend, g.vec_b, nullptr);
     };
 
@@ -178,23 +205,37 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
         tb.store(Bs[0]);
     }
     __syncthreads();
+    const int kk = lane >> 4, cc = lane & 15;
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
         const bool more = k0 + BK < kend;
         if (more) load(k0 + BK);
+        float a[FM][8], b[FN][8];
 #pragma unroll
-        for (int k4 = 0; k4 < BK; k4 += 4) {
-            const int kr = k4 + (lane >> 4), cc = lane & 15;
-            float a[FM], b[FN];
+        for (int i = 0; i < FM; ++i) TileA::frag(As[buf], wm0 + i * 16 + cc, kk, a[i]);
+        if constexpr (RECON) {
+            // op(A)[:, k] *= colscale[k] on this lane's 8 k-values (k = k0 + 8 kk + s)
+            if (g.a_colscale) {
+                float sc[8];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) a[i] = As[buf][kr][wm0 + i * 16 + cc];
+                for (int st = 0; st < 8; ++st) {
+                    const int kx = k0 + 8 * kk + st;
+                    sc[st] = (kx < kend) ? g.a_colscale[kx] : 0.0f;
+                }
 #pragma unroll
-            for (int j = 0; j < FN; ++j) b[j] = Bs[buf][kr][wn0 + j * 16 + cc];
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int st = 0; st < 8; ++st) a[i][st] *= sc[st];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) TileB::frag(Bs[buf], wn0 + j * 16 + cc, kk, b[j]);
+#pragma unroll
+        for (int st = 0; st < 8; ++st)
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][st], b[j][st], acc[i][j], 0, 0, 0);
         if (more) {
             ta.store(As[buf ^ 1]);
             tb.store(Bs[buf ^ 1]);
@@ -205,6 +246,55 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
 
     // epilogue: fragment (i, j) register r holds row 4*(lane/16) + r, column lane % 16
     float *C = g.C + static_cast<uint64_t>(blockIdx.z) * g.split_stride;
+    if constexpr (RECON) {
+        // the reconstruction writes (and may subtract from) a full m x n matrix:
+        // stage the 128 x 128 tile through LDS (the operand buffers are free
+        // now) so that rows leave as 16-byte stores and the minuend arrives as
+        // 16-byte loads, issued before the staging
+        constexpr int CP = BN + 4;
+        float(*Cs)[CP] = reinterpret_cast<float(*)[CP]>(smem);
+        constexpr int Q = BM * BN / 4 / kThreads;  // float4 per thread
+        const bool vec_c = ((g.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15u) == 0) &&
+                           (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
+        float4 mv[Q];
+        if (g.minuend && vec_c) {
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
+                const int gi = m0 + rr, gj = n0 + 4 * c4;
+                mv[q] = (gi < g.M && gj + 4 <= g.N)
+                            ? *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj)
+                            : float4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        __syncthreads();  // every wave is done reading the operand tiles
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    Cs[wm0 + i * 16 + 4 * (lane >> 4) + r][wn0 + j * 16 + (lane & 15)] = acc[i][j][r];
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
+            const int gi = m0 + rr, gj = n0 + 4 * c4;
+            if (gi >= g.M) continue;
+            float4 v = *reinterpret_cast<const float4 *>(&Cs[rr][4 * c4]);
+            const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
+            if (vec_c && gj + 4 <= g.N) {
+                if (g.minuend) v = float4{mv[q].x - v.x, mv[q].y - v.y, mv[q].z - v.z, mv[q].w - v.w};
+                *reinterpret_cast<float4 *>(C + e) = v;
+            } else {
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (gj + u < g.N) C[e + u] = g.minuend ? g.minuend[e + u] - vv[u] : vv[u];
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -213,11 +303,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
             for (int r = 0; r < 4; ++r) {
                 const int gi = m0 + wm0 + i * 16 + 4 * (lane >> 4) + r;
                 const int gj = n0 + wn0 + j * 16 + (lane & 15);
-                if (gi < g.M && gj < g.N) {
-                    const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
-                    const float v = acc[i][j][r];
-                    C[e] = (RECON && g.minuend) ? g.minuend[e] - v : v;
-                }
+                if (gi < g.M && gj < g.N) C[static_cast<uint64_t>(gi) * g.ldc + gj] = acc[i][j][r];
             }
 }
 
