@@ -13,6 +13,7 @@
 // 250-282, 390-408); both are replaced here by Gram-based factorisations whose
 // Gram matrices are formed exactly in FP64 from the FP32 factors.
 #include "bsq_internal.hpp"
+#include "wave_ops.hpp"
 
 #include <algorithm>
 #include <cfloat>
@@ -396,6 +397,71 @@ __global__ void invit_kernel(const double *__restrict__ d, const double *__restr
     for (int i = 0; i < k; ++i) z[i] = b[static_cast<uint64_t>(i) * k];
 }
 
+// LDS variants of trid_factor / trid_apply for invit_lds_kernel: the pivots
+// are stored as reciprocals so the backward pass has no division, and the
+// loops are unrolled so each step's LDS loads are issued ahead of the
+// recurrence that consumes them.
+__device__ void tridl_factor(const double *__restrict__ d, const double *__restrict__ e, int k, double lam,
+                             double tiny, double *__restrict__ u0inv, double *__restrict__ u1,
+                             double *__restrict__ u2, double *__restrict__ ml, int *__restrict__ piv, int st) {
+    double dcur = d[0] - lam, ecur = (k > 1) ? e[0] : 0.0;
+#pragma unroll 4
+    for (int i = 0; i < k - 1; ++i) {
+        const double sub = e[i];                        // T[i+1][i]
+        const double dn = d[i + 1] - lam;               // T[i+1][i+1]
+        const double en = (i + 2 < k) ? e[i + 1] : 0.0;  // T[i+1][i+2]
+        const bool keep = fabs(dcur) >= fabs(sub);
+        const double p = keep ? ((dcur == 0.0) ? tiny : dcur) : sub;
+        // hardware reciprocal + two Newton steps instead of an IEEE division on
+        // the step-to-step chain (|p| >= |numerator|, so m is in [-1, 1])
+        double rp = __builtin_amdgcn_rcp(p);
+        rp = fma(rp, fma(-p, rp, 1.0), rp);
+        rp = fma(rp, fma(-p, rp, 1.0), rp);
+        const double m = (keep ? sub : dcur) * rp;
+        piv[i * st] = keep ? 0 : 1;
+        ml[i * st] = m;
+        u0inv[i * st] = 1.0 / ((fabs(p) < tiny) ? (p < 0.0 ? -tiny : tiny) : p);
+        u1[i * st] = keep ? ecur : dn;
+        u2[i * st] = keep ? 0.0 : en;
+        const double ndcur = keep ? fma(-m, ecur, dn) : fma(-m, dn, ecur);
+        ecur = keep ? en : -m * en;
+        dcur = ndcur;
+    }
+    u0inv[(k - 1) * st] = 1.0 / ((fabs(dcur) < tiny) ? (dcur < 0.0 ? -tiny : tiny) : dcur);
+}
+
+__device__ void tridl_apply(int k, const double *__restrict__ u0inv, const double *__restrict__ u1,
+                            const double *__restrict__ u2, const double *__restrict__ ml,
+                            const int *__restrict__ piv, int st, const double *bin, double *__restrict__ y,
+                            double *x) {
+    // forward elimination bin -> y, back substitution y -> x (x may be bin):
+    // y is a separate array, so no store of a step can alias the loads of the
+    // next ones in either pass
+    double cur = bin[0];
+#pragma unroll 8
+    for (int i = 0; i < k - 1; ++i) {
+        const double nb = bin[(i + 1) * st];
+        const bool sw = piv[i * st] != 0;
+        double nxt = sw ? cur : nb;
+        cur = sw ? nb : cur;
+        nxt = fma(-ml[i * st], cur, nxt);
+        y[i * st] = cur;
+        cur = nxt;
+    }
+    y[(k - 1) * st] = cur;
+    double x1 = 0.0, x2 = 0.0;
+#pragma unroll 8
+    for (int i = k - 1; i >= 0; --i) {
+        double s = y[i * st];
+        s = fma(-u1[i * st], x1, s);  // u1 / u2 are 0 past the end (written by the caller)
+        s = fma(-u2[i * st], x2, s);
+        const double xi = s * u0inv[i * st];
+        x[i * st] = xi;
+        x2 = x1;
+        x1 = xi;
+    }
+}
+
 // The same inverse iteration with every per-eigenvalue array in LDS: lane j
 // (< P) of a one-wave workgroup handles eigenvalue blockIdx.x * P + j, its
 // element i at i * P + j.  The recurrences are sequential per eigenvalue, so
@@ -405,7 +471,8 @@ __global__ __launch_bounds__(64) void invit_lds_kernel(const double *__restrict_
                                                        const double *__restrict__ tnorm_p, double *__restrict__ Z) {
     extern __shared__ double sm[];
     const uint64_t kp = static_cast<uint64_t>(k) * P;
-    double *u0 = sm, *u1 = u0 + kp, *u2 = u1 + kp, *ml = u2 + kp, *b = ml + kp, *ds = b + kp, *es = ds + k;
+    double *u0 = sm, *u1 = u0 + kp, *u2 = u1 + kp, *ml = u2 + kp, *b = ml + kp, *yv = b + kp, *ds = yv + kp,
+           *es = ds + k;
     int *piv = reinterpret_cast<int *>(es + k);
     for (int i = threadIdx.x; i < k; i += blockDim.x) {
         ds[i] = d[i];
@@ -416,13 +483,28 @@ __global__ __launch_bounds__(64) void invit_lds_kernel(const double *__restrict_
     if (j >= P || t >= k) return;  // no barrier below
     const double tnorm = fmax(tnorm_p[0], DBL_MIN);
     const double tiny = tnorm * DBL_EPSILON;
-    trid_factor(ds, es, k, lambda[t], tiny, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P);
+    // the last row of u1 / u2 is read by the backward pass of the last step
+    u1[(k - 1) * P + j] = 0.0;
+    u2[(k - 1) * P + j] = 0.0;
+    if (k >= 2) u2[(k - 2) * P + j] = 0.0;
+    tridl_factor(ds, es, k, lambda[t], tiny, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P);
     for (int i = 0; i < k; ++i) b[i * P + j] = start_entry(t, i);
-    for (int it = 0; it < 3; ++it) {
-        trid_apply(k, tiny, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, b + j, P);
-        double nrm = 0.0;
-        for (int i = 0; i < k; ++i) nrm = fma(b[i * P + j], b[i * P + j], nrm);
+    // two solves: lambda is within k * eps * ||T|| of the eigenvalue, so one
+    // solve already grows the wanted component by ~1 / (k eps) over components
+    // separated by more than the clustering tolerance (closer ones are redone
+    // by cluster_kernel); the second leaves the iterate at working accuracy
+    for (int it = 0; it < 2; ++it) {
+        tridl_apply(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, b + j, yv + j, b + j);
+        double n0 = 0.0, n1 = 0.0;
+#pragma unroll 4
+        for (int i = 0; i < k; i += 2) {
+            const double b0 = b[i * P + j], b1 = (i + 1 < k) ? b[(i + 1) * P + j] : 0.0;
+            n0 = fma(b0, b0, n0);
+            n1 = fma(b1, b1, n1);
+        }
+        const double nrm = n0 + n1;
         const double inv = nrm > 0.0 ? 1.0 / sqrt(nrm) : 0.0;
+#pragma unroll 4
         for (int i = 0; i < k; ++i) b[i * P + j] *= inv;
     }
     double *z = Z + static_cast<uint64_t>(t) * k;
@@ -564,44 +646,68 @@ __global__ __launch_bounds__(64) void multisect_kernel(const double *__restrict_
 // Back-transformation with row-wise reflectors H[j][*]: u_t = H_0 ... H_{k-3} z_t.
 // One wave per eigenvector with z in registers (KPL = ceil(k / 64) values
 // per lane); reflector rows are staged through LDS 16 at a time and shared
-// by the 16 waves of the workgroup.
+// by the 4 waves of the workgroup; the dot products reduce through DPP.
 template <int KPL>
-__global__ __launch_bounds__(1024) void backtransform_rows_kernel(const double *__restrict__ H,
-                                                                  const double *__restrict__ tau, int k,
-                                                                  const double *__restrict__ Z,
-                                                                  float *__restrict__ Uh) {
-    constexpr int RB = 16;
-    __shared__ double hs[RB][KPL * 64];
-    __shared__ double ts[RB];
+__global__ __launch_bounds__(256) void backtransform_rows_kernel(const double *__restrict__ H,
+                                                                 const double *__restrict__ tau, int k,
+                                                                 const double *__restrict__ Z,
+                                                                 float *__restrict__ Uh) {
+    constexpr int RB = 16, NQ = RB * KPL * 64 / 256;  // rows per stage, staged doubles per lane
+    __shared__ double hs[2][RB][KPL * 64];
+    __shared__ double ts[2][RB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t = blockIdx.x * 16 + wave;
+    const int t = blockIdx.x * (blockDim.x >> 6) + wave;
     double z[KPL];
 #pragma unroll
     for (int m = 0; m < KPL; ++m) {
         const int i = lane + 64 * m;
         z[m] = (t < k && i < k) ? Z[static_cast<uint64_t>(t) * k + i] : 0.0;
     }
-    for (int j0 = k - 3; j0 >= 0; j0 -= RB) {
-        const int jl = max(0, j0 - RB + 1);  // rows jl .. j0, applied from j0 down
-        __syncthreads();
-        for (int q = threadIdx.x; q < RB * KPL * 64; q += blockDim.x) {
-            const int rr = q / (KPL * 64), i = q % (KPL * 64);
+    // stage s covers reflectors j0 = k - 3 - RB s down to max(0, j0 - RB + 1);
+    // the next stage is fetched into registers while this one is applied
+    double pre[NQ];
+    double pt = 0.0;
+    auto fetch = [&](int j0) {
+        const int jl = max(0, j0 - RB + 1);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int lin = threadIdx.x + 256 * q, rr = lin / (KPL * 64), i = lin % (KPL * 64);
             const int j = j0 - rr;
-            hs[rr][i] = (j >= jl && i < k) ? H[static_cast<uint64_t>(j) * k + i] : 0.0;
+            pre[q] = (j >= jl && i < k) ? H[static_cast<uint64_t>(j) * k + i] : 0.0;
         }
-        if (threadIdx.x < RB) ts[threadIdx.x] = (j0 - (int)threadIdx.x >= jl) ? tau[j0 - threadIdx.x] : 0.0;
-        __syncthreads();
+        pt = (threadIdx.x < RB && j0 - static_cast<int>(threadIdx.x) >= jl) ? tau[j0 - threadIdx.x] : 0.0;
+    };
+    auto put = [&](int bsel) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int lin = threadIdx.x + 256 * q;
+            hs[bsel][lin / (KPL * 64)][lin % (KPL * 64)] = pre[q];
+        }
+        if (threadIdx.x < RB) ts[bsel][threadIdx.x] = pt;
+    };
+    int cur = 0;
+    if (k - 3 >= 0) {
+        fetch(k - 3);
+        put(0);
+    }
+    __syncthreads();
+    for (int j0 = k - 3; j0 >= 0; j0 -= RB) {
+        const int jl = max(0, j0 - RB + 1);
+        const bool more = j0 - RB >= 0;
+        if (more) fetch(j0 - RB);
         for (int rr = 0; rr <= j0 - jl; ++rr) {
-            const double tj = ts[rr];
-            if (tj == 0.0) continue;
+            const double tj = ts[cur][rr];
+            if (tj == 0.0) continue;  // uniform
             double s = 0.0;
 #pragma unroll
-            for (int m = 0; m < KPL; ++m) s = fma(hs[rr][lane + 64 * m], z[m], s);
-            for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-            s *= tj;
+            for (int m = 0; m < KPL; ++m) s = fma(hs[cur][rr][lane + 64 * m], z[m], s);
+            s = wave_sum_dpp(s) * tj;
 #pragma unroll
-            for (int m = 0; m < KPL; ++m) z[m] = fma(-s, hs[rr][lane + 64 * m], z[m]);
+            for (int m = 0; m < KPL; ++m) z[m] = fma(-s, hs[cur][rr][lane + 64 * m], z[m]);
         }
+        if (more) put(cur ^ 1);
+        __syncthreads();
+        cur ^= 1;
     }
     if (t < k) {
 #pragma unroll
@@ -670,11 +776,11 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
     BSQ_HIP(hipGetLastError());
     multisect_kernel<<<k, 64, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);
     BSQ_HIP(hipGetLastError());
-    // eigenvalues per workgroup whose LDS arrays fit: (5kP + 2k) doubles + kP ints
+    // eigenvalues per workgroup whose LDS arrays fit: (6kP + 2k) doubles + kP ints
     const int64_t lds_cap = 160 * 1024;
-    const int P = static_cast<int>(std::min<int64_t>(8, (lds_cap - 16 * static_cast<int64_t>(k)) / (44 * static_cast<int64_t>(k))));
+    const int P = static_cast<int>(std::min<int64_t>(8, (lds_cap - 16 * static_cast<int64_t>(k)) / (52 * static_cast<int64_t>(k))));
     if (P >= 1) {
-        const size_t lds = (5 * static_cast<size_t>(k) * P + 2 * k) * sizeof(double) + static_cast<size_t>(k) * P * sizeof(int);
+        const size_t lds = (6 * static_cast<size_t>(k) * P + 2 * k) * sizeof(double) + static_cast<size_t>(k) * P * sizeof(int);
         BSQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(invit_lds_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         invit_lds_kernel<<<static_cast<unsigned>(ceil_div(k, P)), 64, lds, stream>>>(d, e, k, P, lambda, tn, Z);
@@ -686,11 +792,12 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
     cluster_kernel<<<k, 256, 0, stream>>>(d, e, k, lambda, tn, Z, scratch, iscratch);
     BSQ_HIP(hipGetLastError());
     if (reg) {
-        const unsigned g = static_cast<unsigned>(ceil_div(k, 16));
-        if (k <= 64) backtransform_rows_kernel<1><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
-        else if (k <= 128) backtransform_rows_kernel<2><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
-        else if (k <= 192) backtransform_rows_kernel<3><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
-        else backtransform_rows_kernel<4><<<g, 1024, 0, stream>>>(W, tau, k, Z, Uh);
+        // 4 eigenvectors per workgroup: k / 4 CUs share the reflector stream
+        const unsigned g = static_cast<unsigned>(ceil_div(k, 4));
+        if (k <= 64) backtransform_rows_kernel<1><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
+        else if (k <= 128) backtransform_rows_kernel<2><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
+        else if (k <= 192) backtransform_rows_kernel<3><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
+        else backtransform_rows_kernel<4><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
     } else
         backtransform_kernel<<<static_cast<unsigned>(ceil_div(k, 4)), 256, 0, stream>>>(W, tau, k, Z, Uh);
     BSQ_HIP(hipGetLastError());

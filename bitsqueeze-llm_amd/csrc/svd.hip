@@ -82,61 +82,82 @@ __global__ void sqrt_eig_kernel(const double *__restrict__ lambda, int k, float 
 }
 
 // Column t of V (rows x k, row-major) divided by its 2-norm (FP64 sum).
-__global__ void col_normalize_kernel(float *__restrict__ V, int rows, int k) {
-    __shared__ double red[4];
-    const int t = blockIdx.x;
-    double s = 0.0;
-    for (int i = threadIdx.x; i < rows; i += blockDim.x) {
-        const double v = V[static_cast<uint64_t>(i) * k + t];
-        s = fma(v, v, s);
+// Column statistics for the final normalisation, row-chunk by row-chunk with
+// coalesced row reads (lane t = column t): over chunk c of the rows,
+//   U:  largest |U[i][t]| and its first row (the sign reference),
+//   Vh: sum of Vh[i][t]^2 (FP64).
+constexpr int kColChunks = 64;
+
+__global__ __launch_bounds__(256) void colstat_kernel(const float *__restrict__ U, int mu,
+                                                       const float *__restrict__ Vh, int nv, int k,
+                                                       float *__restrict__ pbest, int *__restrict__ pidx,
+                                                       double *__restrict__ psum) {
+    const int chunk = blockIdx.x;
+    if (blockIdx.y == 0) {
+        const int r0 = static_cast<int>((static_cast<int64_t>(mu) * chunk) / kColChunks);
+        const int r1 = static_cast<int>((static_cast<int64_t>(mu) * (chunk + 1)) / kColChunks);
+        for (int t = threadIdx.x; t < k; t += blockDim.x) {
+            float best = -1.0f;
+            int bidx = 0x7FFFFFFF;
+#pragma unroll 8
+            for (int i = r0; i < r1; ++i) {
+                const float a = fabsf(U[static_cast<uint64_t>(i) * k + t]);
+                if (a > best) {  // strict: the first row wins ties
+                    best = a;
+                    bidx = i;
+                }
+            }
+            pbest[static_cast<uint64_t>(chunk) * k + t] = best;
+            pidx[static_cast<uint64_t>(chunk) * k + t] = bidx;
+        }
+    } else {
+        const int r0 = static_cast<int>((static_cast<int64_t>(nv) * chunk) / kColChunks);
+        const int r1 = static_cast<int>((static_cast<int64_t>(nv) * (chunk + 1)) / kColChunks);
+        for (int t = threadIdx.x; t < k; t += blockDim.x) {
+            double s = 0.0;
+#pragma unroll 8
+            for (int i = r0; i < r1; ++i) {
+                const double v = Vh[static_cast<uint64_t>(i) * k + t];
+                s = fma(v, v, s);
+            }
+            psum[static_cast<uint64_t>(chunk) * k + t] = s;
+        }
     }
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-    __syncthreads();
-    const double tot = red[0] + red[1] + red[2] + red[3];
-    if (!(tot > 0.0)) return;
-    const float inv = static_cast<float>(1.0 / sqrt(tot));
-    for (int i = threadIdx.x; i < rows; i += blockDim.x) V[static_cast<uint64_t>(i) * k + t] *= inv;
 }
 
-// Flip column t of U and V when the first largest-|.| entry of U[:, t] is
-// negative.
-__global__ void sign_fix_kernel(float *__restrict__ U, int m, float *__restrict__ V, int n, int k) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
-    const int t = blockIdx.x;
+// Per column, in chunk order: the sign that makes the first largest-|.| entry
+// of U[:, t] non-negative, and 1 / ||Vh[:, t]|| (1 for a zero column).
+__global__ void colfinal_kernel(const float *__restrict__ U, int k, const float *__restrict__ pbest,
+                                const int *__restrict__ pidx, const double *__restrict__ psum,
+                                float *__restrict__ usign, float *__restrict__ vscale) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= k) return;
     float best = -1.0f;
     int bidx = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < m; i += blockDim.x) {
-        const float a = fabsf(U[static_cast<uint64_t>(i) * k + t]);
-        if (a > best) {
-            best = a;
+    double s = 0.0;
+#pragma unroll 16
+    for (int c = 0; c < kColChunks; ++c) {
+        const float b = pbest[static_cast<uint64_t>(c) * k + t];
+        const int i = pidx[static_cast<uint64_t>(c) * k + t];
+        if (b > best || (b == best && i < bidx)) {
+            best = b;
             bidx = i;
         }
+        s += psum[static_cast<uint64_t>(c) * k + t];
     }
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ob = __shfl_xor(best, off);
-        const int oi = __shfl_xor(bidx, off);
-        if (ob > best || (ob == best && oi < bidx)) {
-            best = ob;
-            bidx = oi;
-        }
-    }
-    if ((threadIdx.x & 63) == 0) {
-        bv[threadIdx.x >> 6] = best;
-        bi[threadIdx.x >> 6] = bidx;
-    }
-    __syncthreads();
-    float b = bv[0];
-    int idx = bi[0];
-    for (int w = 1; w < 4; ++w)
-        if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
-            b = bv[w];
-            idx = bi[w];
-        }
-    if (idx >= m || !(U[static_cast<uint64_t>(idx) * k + t] < 0.0f)) return;
-    for (int i = threadIdx.x; i < m; i += blockDim.x) U[static_cast<uint64_t>(i) * k + t] *= -1.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) V[static_cast<uint64_t>(i) * k + t] *= -1.0f;
+    const float sg = (bidx != 0x7FFFFFFF && U[static_cast<uint64_t>(bidx) * k + t] < 0.0f) ? -1.0f : 1.0f;
+    usign[t] = sg;
+    vscale[t] = (s > 0.0) ? sg * static_cast<float>(1.0 / sqrt(s)) : sg;
+}
+
+// Uw[:, t] *= usign[t];  Vh[:, t] *= vscale[t]  (coalesced rows)
+__global__ void colscale_kernel(float *__restrict__ Uw, uint64_t nu, float *__restrict__ Vh, uint64_t nv, int k,
+                                const float *__restrict__ usign, const float *__restrict__ vscale) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < nu; e += stride)
+        Uw[e] *= usign[e % k];
+    for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < nv; e += stride)
+        Vh[e] *= vscale[e % k];
 }
 
 template <typename T>
@@ -163,6 +184,9 @@ struct SvdPlan {
     float *Linv = nullptr, *Uh = nullptr;
     double *G = nullptr, *W = nullptr, *Z = nullptr, *small = nullptr, *scratch = nullptr, *lambda = nullptr;
     double *Lbuf = nullptr;  // blocked Cholesky: L and the inverses of its diagonal blocks
+    float *cbest = nullptr, *csign = nullptr;  // column statistics of the final normalisation
+    int *cidx = nullptr;
+    double *csum = nullptr;
     int *iscratch = nullptr, *status = nullptr;
     double *gram_ws = nullptr;
     float *gemm_ws = nullptr;
@@ -179,6 +203,10 @@ struct SvdPlan {
         release(G);
         release(W);
         release(Lbuf);
+        release(cbest);
+        release(csign);
+        release(cidx);
+        release(csum);
         release(Z);
         release(small);
         release(scratch);
@@ -215,6 +243,10 @@ SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
         if (chol_blocked_supported(static_cast<int>(k))) p->Lbuf = alloc<double>(chol_blocked_buffer_doubles(static_cast<int>(k)));
         p->Z = alloc<double>(k * k);
         p->small = alloc<double>(4 * k + 8);
+        p->cbest = alloc<float>(kColChunks * k);
+        p->cidx = alloc<int>(kColChunks * k);
+        p->csum = alloc<double>(kColChunks * k);
+        p->csign = alloc<float>(2 * k);
         p->scratch = alloc<double>(9 * k * k);
         p->lambda = alloc<double>(k);
         p->iscratch = alloc<int>(2 * k * k);
@@ -300,10 +332,24 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
                 st);
     launch_gemm(false, false, Nw, k, k, Ya, k, p->Uh, k, Vh_out, k, nullptr, nullptr, p->gemm_ws, p->gemm_ws_bytes,
                 st);
-    col_normalize_kernel<<<k, 256, 0, st>>>(Vh_out, Nw, k);
+    // V_hat = Y U_hat / S (columns normalised), then the sign convention: the
+    // first largest-|.| entry of every column of U is non-negative (U and V
+    // flipped together).  Positive scaling does not move that entry, so both
+    // come from one pass of column statistics.
+    const float *Usrc = p->transposed ? Vh_out : Uw_out;  // U in the output orientation
+    colstat_kernel<<<dim3(kColChunks, 2), 256, 0, st>>>(Usrc, m, Vh_out, Nw, k, p->cbest, p->cidx, p->csum);
     BSQ_HIP(hipGetLastError());
-    sign_fix_kernel<<<k, 256, 0, st>>>(U, m, V, n, k);
+    colfinal_kernel<<<static_cast<unsigned>(ceil_div(k, 256)), 256, 0, st>>>(Usrc, k, p->cbest, p->cidx, p->csum,
+                                                                             p->csign, p->csign + k);
     BSQ_HIP(hipGetLastError());
+    {
+        const uint64_t nu = static_cast<uint64_t>(Mw) * k, nvh = static_cast<uint64_t>(Nw) * k;
+        uint64_t grid = ceil_div(std::max(nu, nvh), 256);
+        grid = std::min<uint64_t>(grid, static_cast<uint64_t>(cu_count()) * 8);
+        colscale_kernel<<<static_cast<unsigned>(grid), 256, 0, st>>>(Uw_out, nu, Vh_out, nvh, k, p->csign,
+                                                                     p->csign + k);
+        BSQ_HIP(hipGetLastError());
+    }
 }
 
 void launch_reconstruct(const float *U, const float *S, const float *V, int m, int n, int k, const float *minuend,
