@@ -233,15 +233,17 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
             // trailing update A_ab -= L_aj L_bj^T for jb < b <= a
             if (jb + 1 < NB) {
 #pragma unroll 1
-                for (int t = 0; t < 32; ++t) {
-                    double rv[NB];
+                for (int t = 0; t < 32; t += 2) {  // two panel columns per pass: 16-byte LDS reads
+                    double2 rv[NB];
 #pragma unroll
-                    for (int a = jb + 1; a < NB; ++a) rv[a] = P[(a - jb - 1) * 32 + ty][t];
+                    for (int a = jb + 1; a < NB; ++a)
+                        rv[a] = *reinterpret_cast<const double2 *>(&P[(a - jb - 1) * 32 + ty][t]);
 #pragma unroll
                     for (int b = jb + 1; b < NB; ++b) {
-                        const double cv = P[(b - jb - 1) * 32 + tx][t];
+                        const double2 cv = *reinterpret_cast<const double2 *>(&P[(b - jb - 1) * 32 + tx][t]);
 #pragma unroll
-                        for (int a = b; a < NB; ++a) r[tri(a, b)] = fma(-rv[a], cv, r[tri(a, b)]);
+                        for (int a = b; a < NB; ++a)
+                            r[tri(a, b)] = fma(-rv[a].y, cv.y, fma(-rv[a].x, cv.x, r[tri(a, b)]));
                     }
                 }
             }
