@@ -24,58 +24,111 @@ namespace {
 constexpr int kGramTile = 64;
 
 // ---------------------------------------------------------------------------
-// Gram: partial G over a row chunk for one lower 64x64 tile
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gram_partial_kernel(const float *__restrict__ X, int M, int k, int ld,
-                                                            int rows_per_split, double *__restrict__ P) {
-    __shared__ float xi[16][kGramTile + 1];
-    __shared__ float xj[16][kGramTile + 1];
-    // blockIdx.x -> lower tile (ti >= tj)
+// Gram: partial G over a row chunk for one lower 64x64 tile, on the FP64
+// matrix cores (v_mfma_f64_16x16x4f64):
+// 256 lanes = 4 waves, each a 32 x 32 quarter of the 64 x 64 tile as 2 x 2
+// MFMA blocks.  Rows are staged 32 at a time through LDS (16-byte loads,
+// the next chunk fetched while the current one is multiplied); the FP32
+// inputs are widened to FP64 exactly, so every product and sum is FP64.
+// MFMA operand lanes: A[i][k] and B[k][j] in lane 16 k + (i or j);
+// accumulator register r of lane l holds D[4 r + l / 16][l % 16].
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+constexpr int kGramRows = 32, kGramPitch = kGramTile + 16;  // pitch: 16-bank offset between k rows
+
+__global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict__ X, int M, int k, int ld,
+                                                         int rows_per_split, bool vec, double *__restrict__ P) {
+    __shared__ __attribute__((aligned(16))) float xi[2][kGramRows][kGramPitch];
+    __shared__ __attribute__((aligned(16))) float xj[2][kGramRows][kGramPitch];
     int t = blockIdx.x, ti = 0;
     while (t > ti) {
         t -= ti + 1;
         ++ti;
     }
     const int tj = t;
+    const bool diag = ti == tj;
     const int r0 = blockIdx.y * rows_per_split, r1 = min(M, r0 + rows_per_split);
-    const int ty = threadIdx.x >> 4, tx = threadIdx.x & 15;
-    double acc[4][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wi = (wave >> 1) * 32, wj = (wave & 1) * 32;
+    // staging: 32 rows x 64 columns = 512 float4, two per lane per operand
+    float4 pi[2], pj[2];
+    auto fetch = [&](int rb) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = 0.0;
-    for (int rb = r0; rb < r1; rb += 16) {
-        for (int e = threadIdx.x; e < 16 * kGramTile; e += 256) {
-            const int rr = e / kGramTile, cc = e % kGramTile;
-            const int r = rb + rr;
-            const int ci = ti * kGramTile + cc, cj = tj * kGramTile + cc;
-            xi[rr][cc] = (r < r1 && ci < k) ? X[static_cast<uint64_t>(r) * ld + ci] : 0.0f;
-            xj[rr][cc] = (r < r1 && cj < k) ? X[static_cast<uint64_t>(r) * ld + cj] : 0.0f;
-        }
-        __syncthreads();
-#pragma unroll 4
-        for (int rr = 0; rr < 16; ++rr) {
-            double a[4], b[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                a[q] = static_cast<double>(xi[rr][ty * 4 + q]);
-                b[q] = static_cast<double>(xj[rr][tx * 4 + q]);
+        for (int q = 0; q < 2; ++q) {
+            const int lin = tid + 256 * q, rr = lin >> 4, c4 = (lin & 15) * 4;
+            const int r = rb + rr, ci = ti * kGramTile + c4, cj = tj * kGramTile + c4;
+            const float *row = X + static_cast<uint64_t>(r) * ld;
+            if (vec && r < r1 && ci + 4 <= k) {
+                pi[q] = *reinterpret_cast<const float4 *>(row + ci);
+            } else {
+                pi[q].x = (r < r1 && ci + 0 < k) ? row[ci + 0] : 0.0f;
+                pi[q].y = (r < r1 && ci + 1 < k) ? row[ci + 1] : 0.0f;
+                pi[q].z = (r < r1 && ci + 2 < k) ? row[ci + 2] : 0.0f;
+                pi[q].w = (r < r1 && ci + 3 < k) ? row[ci + 3] : 0.0f;
             }
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) acc[p][q] = fma(a[p], b[q], acc[p][q]);
+            if (!diag) {
+                if (vec && r < r1 && cj + 4 <= k) {
+                    pj[q] = *reinterpret_cast<const float4 *>(row + cj);
+                } else {
+                    pj[q].x = (r < r1 && cj + 0 < k) ? row[cj + 0] : 0.0f;
+                    pj[q].y = (r < r1 && cj + 1 < k) ? row[cj + 1] : 0.0f;
+                    pj[q].z = (r < r1 && cj + 2 < k) ? row[cj + 2] : 0.0f;
+                    pj[q].w = (r < r1 && cj + 3 < k) ? row[cj + 3] : 0.0f;
+                }
+            }
         }
+    };
+    auto put = [&](int b) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int lin = tid + 256 * q, rr = lin >> 4, c4 = (lin & 15) * 4;
+            *reinterpret_cast<float4 *>(&xi[b][rr][c4]) = pi[q];
+            if (!diag) *reinterpret_cast<float4 *>(&xj[b][rr][c4]) = pj[q];
+        }
+    };
+    f64x4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = f64x4{0.0, 0.0, 0.0, 0.0};
+    int buf = 0;
+    if (r0 < r1) {
+        fetch(r0);
+        put(0);
+    }
+    __syncthreads();
+    const int kk = lane >> 4, cc = lane & 15;
+    for (int rb = r0; rb < r1; rb += kGramRows) {
+        const bool more = rb + kGramRows < r1;
+        if (more) fetch(rb + kGramRows);
+        const float(*BI)[kGramPitch] = xi[buf];
+        const float(*BJ)[kGramPitch] = diag ? xi[buf] : xj[buf];
+#pragma unroll
+        for (int st = 0; st < kGramRows / 4; ++st) {
+            const int rr = 4 * st + kk;
+            double av[2], bv[2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) av[a] = static_cast<double>(BI[rr][wi + 16 * a + cc]);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) bv[b] = static_cast<double>(BJ[rr][wj + 16 * b + cc]);
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
+        if (more) put(buf ^ 1);
         __syncthreads();
+        buf ^= 1;
     }
     double *out = P + static_cast<uint64_t>(blockIdx.y) * k * k;
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int i = ti * kGramTile + ty * 4 + p, j = tj * kGramTile + tx * 4 + q;
-            if (i < k && j < k && j <= i) out[static_cast<uint64_t>(i) * k + j] = acc[p][q];
-        }
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = ti * kGramTile + wi + 16 * a + 4 * r + kk, j = tj * kGramTile + wj + 16 * b + cc;
+                if (i < k && j < k && j <= i) out[static_cast<uint64_t>(i) * k + j] = acc[a][b][r];
+            }
 }
 
 // G[i][j] = G[j][i] = sum_s P[s][i][j] (lower entries), fixed order.
@@ -726,22 +779,27 @@ void launch_sytrd_blocked(const double *G, int k, double *d, double *e, double *
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-uint64_t gram_workspace_bytes(int M, int k) {
+// Row splits of the Gram: about one workgroup per CU over all lower tiles,
+// at least 256 rows each (fewer partial matrices to sum).
+int gram_splits(int M, int k) {
     const int nt = static_cast<int>(ceil_div(k, kGramTile));
     const int tiles = nt * (nt + 1) / 2;
-    int splits = static_cast<int>(ceil_div(static_cast<uint64_t>(cu_count()) * 2, tiles));
-    splits = std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 256))));
-    return static_cast<uint64_t>(splits) * k * k * sizeof(double);
+    int splits = static_cast<int>(ceil_div(static_cast<uint64_t>(cu_count()), tiles));
+    return std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 256))));
+}
+
+uint64_t gram_workspace_bytes(int M, int k) {
+    return static_cast<uint64_t>(gram_splits(M, k)) * k * k * sizeof(double);
 }
 
 void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream) {
     const int nt = static_cast<int>(ceil_div(k, kGramTile));
     const int tiles = nt * (nt + 1) / 2;
-    int splits = static_cast<int>(ceil_div(static_cast<uint64_t>(cu_count()) * 2, tiles));
-    splits = std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 256))));
-    const int rows_per = static_cast<int>(ceil_div(ceil_div(M, splits), 16) * 16);
+    int splits = gram_splits(M, k);
+    const int rows_per = static_cast<int>(ceil_div(ceil_div(M, splits), kGramRows) * kGramRows);
     splits = static_cast<int>(ceil_div(M, rows_per));
-    gram_partial_kernel<<<dim3(tiles, splits), 256, 0, stream>>>(X, M, k, ld, rows_per, workspace);
+    const bool vec = (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15u) == 0);
+    gram_mfma_kernel<<<dim3(tiles, splits), 256, 0, stream>>>(X, M, k, ld, rows_per, vec, workspace);
     BSQ_HIP(hipGetLastError());
     const uint64_t kk = static_cast<uint64_t>(k) * k;
     const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(ceil_div(kk, 256), 1024));
