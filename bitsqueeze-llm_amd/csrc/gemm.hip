@@ -9,14 +9,18 @@
 // Used for the randomised range finder (X = op(A) R, Y = op(A)^T X with the
 // big activation matrix read row-major in place, so no transposed copy is
 // ever made), the small basis rotations (X * W) and the low-rank
-// reconstruction U diag(S) V^T, which folds diag(S) into the A-tile load and
-// can subtract from a minuend in the epilogue (error = residual - U S V^T).
+// reconstruction U diag(S) V^T, which scales the A fragments by S (fetched a
+// slice ahead with the operand tiles) and can subtract from a minuend in the
+// epilogue (error = residual - U S V^T).
 //
 // Tiling: 256 threads = 4 waves in a 2 x 2 grid; workgroup tile 128 x 128,
-// BK = 32; each wave owns 64 x 64 as 4 x 4 MFMA 16x16 blocks (64 AGPRs).
-// Tiles move global -> registers (16-byte loads where the layout allows)
-// -> LDS in their global orientation (16-byte writes; layouts below) while
-// the previous tile is multiplied.  Skinny shapes are split
+// BK = 16, so the double-buffered tiles take ~40 KB of LDS and three or four
+// workgroups share a CU (more waves to cover each other's barrier and
+// global-load waits than the two that 32-deep tiles allow); each wave owns
+// 64 x 64 as 4 x 4 MFMA 16x16 blocks (64 AGPRs).  Tiles move global ->
+// registers (16-byte loads where the layout allows) -> LDS in their global
+// orientation (16-byte writes; layouts below) while the previous tile is
+// multiplied.  Skinny shapes are split
 // along K so the grid fills the 256 CUs several times over; partial products
 // go to a workspace summed in a fixed order, so results are deterministic.
 #include "bsq_internal.hpp"
@@ -27,7 +31,8 @@ namespace {
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int KS = BK / 4;  // k-values per lane per slice
 
 struct GemmArgs {
     const float *A;
@@ -45,17 +50,17 @@ struct GemmArgs {
 // LDS tile layouts.  The 16x16x4 MFMA takes, in lane l = 16 kk + i, the
 // operand element (row / column i, k), and the k order inside a BK slice is
 // free as long as both operands use the same one.  Lane kk takes
-// k = 8 kk + s at MFMA step s (s = 0..7), so:
+// k = KS kk + s at MFMA step s (s = 0..KS-1, KS = BK / 4 = 4), so:
 //   k-contiguous tiles (A with TA = false, B with TB = true) are kept as
-//   [row][k] (pitch 36 floats): a lane's 8 k-values of a fragment are two
-//   16-byte reads, and the rows of 16 lanes start 36 banks apart (no
-//   conflicts); the global tile is stored as loaded (16-byte LDS writes);
+//   [row][k] (pitch 20 floats): a lane's KS k-values of a fragment are one
+//   16-byte read, and the rows of 16 lanes start 20 banks apart; the global
+//   tile is stored as loaded (16-byte LDS writes);
 //   k-major tiles (A with TA = true, B with TB = false) are kept as [k][col]
 //   (pitch R + 4): one 4-byte read per step, 16-byte LDS writes.
 constexpr int PK = BK + 4;
 
-// k-contiguous operand tile: R rows x 32 k-values.  256 threads: thread t
-// covers row (t % R) + R * pass, k quad (t / R) ... (8 quads per row).
+// k-contiguous operand tile: R rows x BK k-values.  256 threads: thread t
+// covers row (t % R) + R * pass, k quad (t / R) (BK / 4 quads per row).
 template <int R>
 struct KContig {
     static constexpr int N4 = R * BK / 4 / kThreads;  // float4 per thread
@@ -66,7 +71,7 @@ struct KContig {
         const int t = threadIdx.x;
 #pragma unroll
         for (int q = 0; q < N4; ++q) {
-            const int lin = t + q * kThreads;  // 0 .. R*8-1
+            const int lin = t + q * kThreads;  // 0 .. R * BK / 4 - 1
             const int r = lin % R, kq = lin / R;
             const int gr = r0 + r, gk = k0 + kq * 4;
             float4 x;
@@ -96,22 +101,17 @@ struct KContig {
             *reinterpret_cast<float4 *>(&S[lin % R][(lin / R) * 4]) = v[q];
         }
     }
-    // the 8 k-values (k = 8 kk + s) of row `row` for this lane
-    __device__ __forceinline__ static void frag(const Tile &S, int row, int kk, float (&o)[8]) {
-        const float4 lo = *reinterpret_cast<const float4 *>(&S[row][8 * kk]);
-        const float4 hi = *reinterpret_cast<const float4 *>(&S[row][8 * kk + 4]);
+    // the KS k-values (k = KS kk + s) of row `row` for this lane
+    __device__ __forceinline__ static void frag(const Tile &S, int row, int kk, float (&o)[KS]) {
+        const float4 lo = *reinterpret_cast<const float4 *>(&S[row][4 * kk]);
         o[0] = lo.x;
         o[1] = lo.y;
         o[2] = lo.z;
         o[3] = lo.w;
-        o[4] = hi.x;
-        o[5] = hi.y;
-        o[6] = hi.z;
-        o[7] = hi.w;
     }
 };
 
-// k-major operand tile: 32 k-rows x Cn contiguous values.
+// k-major operand tile: BK k-rows x Cn contiguous values.
 template <int Cn>
 struct KMajor {
     static constexpr int N4 = Cn * BK / 4 / kThreads;
@@ -155,9 +155,9 @@ struct KMajor {
             *reinterpret_cast<float4 *>(&S[lin / C4][(lin % C4) * 4]) = v[q];
         }
     }
-    __device__ __forceinline__ static void frag(const Tile &S, int col, int kk, float (&o)[8]) {
+    __device__ __forceinline__ static void frag(const Tile &S, int col, int kk, float (&o)[KS]) {
 #pragma unroll
-        for (int s = 0; s < 8; ++s) o[s] = S[8 * kk + s][col];
+        for (int s = 0; s < KS; ++s) o[s] = S[KS * kk + s][col];
     }
 };
 
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
     // one LDS block: the double-buffered operand tiles, reused by the
     // reconstruction epilogue to stage the output tile
     constexpr size_t kABytes = 2 * sizeof(typename TileA::Tile), kBBytes = 2 * sizeof(typename TileB::Tile);
-    constexpr size_t kCBytes = RECON ? sizeof(float) * BM * (BN + 4) : 0;
+    constexpr size_t kCBytes = RECON ? sizeof(float) * (BM / 2) * (BN + 4) : 0;
     constexpr size_t kSmem = (kABytes + kBBytes > kCBytes) ? kABytes + kBBytes : kCBytes;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
     typename TileA::Tile *As = reinterpret_cast<typename TileA::Tile *>(smem);
@@ -199,38 +199,45 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
     };
 
     int buf = 0;
+    const int kk = lane >> 4, cc = lane & 15;
+    // RECON: op(A)[:, k] *= colscale[k] on this lane's KS k-values
+    // (k = k0 + KS kk + s), fetched one slice ahead with the operand tiles
+    float sc[KS];
+    auto load_scale = [&](int k0) {
+        if constexpr (RECON) {
+#pragma unroll
+            for (int st = 0; st < KS; ++st) {
+                const int kx = k0 + KS * kk + st;
+                sc[st] = (g.a_colscale && kx < kend) ? g.a_colscale[kx] : 1.0f;
+            }
+        }
+    };
     if (kbeg < kend) {
         load(kbeg);
+        load_scale(kbeg);
         ta.store(As[0]);
         tb.store(Bs[0]);
     }
     __syncthreads();
-    const int kk = lane >> 4, cc = lane & 15;
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
         const bool more = k0 + BK < kend;
-        if (more) load(k0 + BK);
-        float a[FM][8], b[FN][8];
+        float a[FM][KS], b[FN][KS];
 #pragma unroll
         for (int i = 0; i < FM; ++i) TileA::frag(As[buf], wm0 + i * 16 + cc, kk, a[i]);
         if constexpr (RECON) {
-            // op(A)[:, k] *= colscale[k] on this lane's 8 k-values (k = k0 + 8 kk + s)
-            if (g.a_colscale) {
-                float sc[8];
 #pragma unroll
-                for (int st = 0; st < 8; ++st) {
-                    const int kx = k0 + 8 * kk + st;
-                    sc[st] = (kx < kend) ? g.a_colscale[kx] : 0.0f;
-                }
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int st = 0; st < 8; ++st) a[i][st] *= sc[st];
-            }
+                for (int st = 0; st < KS; ++st) a[i][st] *= sc[st];
+        }
+        if (more) {
+            load(k0 + BK);
+            load_scale(k0 + BK);
         }
 #pragma unroll
         for (int j = 0; j < FN; ++j) TileB::frag(Bs[buf], wn0 + j * 16 + cc, kk, b[j]);
 #pragma unroll
-        for (int st = 0; st < 8; ++st)
+        for (int st = 0; st < KS; ++st)
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -248,49 +255,54 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
     float *C = g.C + static_cast<uint64_t>(blockIdx.z) * g.split_stride;
     if constexpr (RECON) {
         // the reconstruction writes (and may subtract from) a full m x n matrix:
-        // stage the 128 x 128 tile through LDS (the operand buffers are free
-        // now) so that rows leave as 16-byte stores and the minuend arrives as
-        // 16-byte loads, issued before the staging
-        constexpr int CP = BN + 4;
+        // stage the tile through LDS (the operand buffers are free now) in two
+        // 64-row halves so that rows leave as 16-byte stores and the minuend
+        // arrives as 16-byte loads, issued before the staging
+        constexpr int CP = BN + 4, HM = BM / 2;
         float(*Cs)[CP] = reinterpret_cast<float(*)[CP]>(smem);
-        constexpr int Q = BM * BN / 4 / kThreads;  // float4 per thread
+        constexpr int Q = HM * BN / 4 / kThreads;  // float4 per thread per half
         const bool vec_c = ((g.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15u) == 0) &&
                            (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
-        float4 mv[Q];
-        if (g.minuend && vec_c) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float4 mv[Q];
+            if (g.minuend && vec_c) {
+#pragma unroll
+                for (int q = 0; q < Q; ++q) {
+                    const int lin = tid + q * kThreads, rr = h * HM + lin / (BN / 4), c4 = lin % (BN / 4);
+                    const int gi = m0 + rr, gj = n0 + 4 * c4;
+                    mv[q] = (gi < g.M && gj + 4 <= g.N)
+                                ? *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj)
+                                : float4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+            __syncthreads();  // the operand tiles (h = 0) or the previous half (h = 1) are consumed
+            if (wm0 == h * HM) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            Cs[i * 16 + 4 * (lane >> 4) + r][wn0 + j * 16 + (lane & 15)] = acc[i][j][r];
+            }
+            __syncthreads();
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
-                const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
-                const int gi = m0 + rr, gj = n0 + 4 * c4;
-                mv[q] = (gi < g.M && gj + 4 <= g.N)
-                            ? *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj)
-                            : float4{0.f, 0.f, 0.f, 0.f};
-            }
-        }
-        __syncthreads();  // every wave is done reading the operand tiles
+                const int lin = tid + q * kThreads, rl = lin / (BN / 4), c4 = lin % (BN / 4);
+                const int gi = m0 + h * HM + rl, gj = n0 + 4 * c4;
+                if (gi >= g.M) continue;
+                float4 v = *reinterpret_cast<const float4 *>(&Cs[rl][4 * c4]);
+                const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
+                if (vec_c && gj + 4 <= g.N) {
+                    if (g.minuend) v = float4{mv[q].x - v.x, mv[q].y - v.y, mv[q].z - v.z, mv[q].w - v.w};
+                    *reinterpret_cast<float4 *>(C + e) = v;
+                } else {
+                    const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    Cs[wm0 + i * 16 + 4 * (lane >> 4) + r][wn0 + j * 16 + (lane & 15)] = acc[i][j][r];
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
-            const int gi = m0 + rr, gj = n0 + 4 * c4;
-            if (gi >= g.M) continue;
-            float4 v = *reinterpret_cast<const float4 *>(&Cs[rr][4 * c4]);
-            const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
-            if (vec_c && gj + 4 <= g.N) {
-                if (g.minuend) v = float4{mv[q].x - v.x, mv[q].y - v.y, mv[q].z - v.z, mv[q].w - v.w};
-                *reinterpret_cast<float4 *>(C + e) = v;
-            } else {
-                const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (gj + u < g.N) C[e + u] = g.minuend ? g.minuend[e + u] - vv[u] : vv[u];
+                    for (int u = 0; u < 4; ++u)
+                        if (gj + u < g.N) C[e + u] = g.minuend ? g.minuend[e + u] - vv[u] : vv[u];
+                }
             }
         }
         return;
@@ -321,20 +333,20 @@ __global__ void splitk_reduce_kernel(const float *__restrict__ W, int splits, ui
 }
 
 // Split count minimising the modelled time: rounds of resident workgroups
-// (two 128x128 tiles fit one CU's LDS) times the K slice each one walks,
+// (three 128x128 tiles fit one CU's LDS) times the K slice each one walks,
 // plus the traffic of summing the partials.
 int choose_splits(int M, int N, int K) {
     const uint64_t tiles = ceil_div(M, BM) * ceil_div(N, BN);
-    const uint64_t slots = static_cast<uint64_t>(cu_count()) * 2;
+    const uint64_t slots = static_cast<uint64_t>(cu_count()) * 3;
     const uint64_t ksteps = ceil_div(K, BK);
     double best = 0.0;
     int best_s = 1;
     for (int s = 1; s <= 32; ++s) {
-        if (s > 1 && ksteps / s < 8) break;  // keep >= 8 K steps per split
+        if (s > 1 && ksteps * BK / s < 256) break;  // keep >= 256 K values per split
         const uint64_t rounds = ceil_div(tiles * s, slots);
-        // one K step of a 128x128x32 tile ~ 2 * 128 * 128 * 32 / (256 flop/clk) cycles;
+        // one K step of a 128x128xBK tile ~ 2 * 128 * 128 * BK / (256 flop/clk) cycles;
         // the reduce moves (s + 1) * M * N * 4 bytes at ~ 2 KB / clk chip-wide.
-        const double t = static_cast<double>(rounds) * ceil_div(ksteps, s) * 4096.0 +
+        const double t = static_cast<double>(rounds) * ceil_div(ksteps, s) * (128.0 * BK) +
                          (s > 1 ? (s + 1.0) * M * N * 4.0 / 2048.0 : 0.0);
         if (s == 1 || t < best) {
             best = t;

@@ -33,9 +33,12 @@ __global__ __launch_bounds__(kTrdThreads) void sytrd_blocked_kernel(const double
                                                                      double *__restrict__ d, double *__restrict__ e,
                                                                      double *__restrict__ tau,
                                                                      double *__restrict__ H) {
-    constexpr int KP = NB * 32, NE = NB * (NB + 1) / 2, PITCH = 66;
+    // PP pitch 65 (odd): the column-partial writes (16 lanes down a column)
+    // and the finishing reads (four lanes per index, 8 banks apart) are free
+    // of LDS bank conflicts with 8-byte accesses
+    constexpr int KP = NB * 32, NE = NB * (NB + 1) / 2, PITCH = 65;
     __shared__ double xs[KP], vs[KP], ws[KP];
-    __shared__ __attribute__((aligned(16))) double PP[NB][32][PITCH];  // [blk][y][0..31 row, 32..63 col partials]
+    __shared__ double PP[NB][32][PITCH];  // [blk][y][0..31 row, 32..63 col partials]
     __shared__ double red[kTrdThreads / 64];
     __shared__ double s_tau;
 
@@ -141,16 +144,19 @@ __global__ __launch_bounds__(kTrdThreads) void sytrd_blocked_kernel(const double
             if (tid < 4 * KP) {  // whole waves: 4 KP is a multiple of 128
                 const int idx = tid >> 2, qq = tid & 3;  // idx = 32 * blk + y
                 const int blk = idx >> 5, y = idx & 31;
+                // this lane's 16 partials: slots 16 m + 4 qq + s
                 double s = 0.0;
 #pragma unroll
-                for (int u = 0; u < 16; u += 2) {
-                    const double2 pr = *reinterpret_cast<const double2 *>(&PP[blk][y][16 * qq + u]);
-                    s += pr.x + pr.y;
-                }
-                s = quad_sum(s);
-                double K = 0.0;
+                for (int m = 0; m < 4; ++m)
 #pragma unroll
-                for (int w = 0; w < kTrdThreads / 64; ++w) K += red[w];
+                    for (int u = 0; u < 4; u += 2) s += PP[blk][y][16 * m + 4 * qq + u] + PP[blk][y][16 * m + 4 * qq + u + 1];
+                s = quad_sum(s);
+                // K = sum of the 16 wave partials: one LDS read per lane and a
+                // 16-lane DPP sum instead of 16 reads per lane
+                double K = red[lane & 15];
+                K = quad_sum(K);
+                K += dpp_read<0x141>(K);  // row_half_mirror: 8-lane sums
+                K += dpp_read<0x140>(K);  // row_mirror: 16-lane sums in every lane
                 // v^T A v counted every off-diagonal pair twice through rows and
                 // columns, which is exactly the symmetric sum
                 if (qq == 0) ws[idx] = (idx > j) ? fma(-0.5 * t * t * K, vs[idx], t * s) : 0.0;
