@@ -161,6 +161,28 @@ struct KMajor {
     }
 };
 
+// Tile of workgroup `bid` (1-D grid over the ny x nx output tiles).  The
+// hardware deals workgroups to the 8 XCDs round-robin (bid % 8), and each
+// XCD has its own L2: give XCD x a contiguous range of logical tiles, and
+// walk the logical order in groups of kGroupRows tile rows with the column
+// index outermost, so the workgroups resident on one XCD share a few A
+// panels and a few B panels instead of touching every panel of both
+// operands (which re-fetches them from HBM).  A bijection onto the tiles for
+// any grid size.
+constexpr int kXcds = 8, kGroupRows = 8;
+__device__ __forceinline__ void xcd_tile(int bid, int ny, int nx, int &tm, int &tn) {
+    const int T = ny * nx;
+    const int xcd = bid % kXcds, loc = bid / kXcds;
+    const int per = T / kXcds, rem = T % kXcds;
+    const int L = xcd * per + min(xcd, rem) + loc;
+    const int span = kGroupRows * nx;
+    const int first = (L / span) * kGroupRows;
+    const int rows = min(ny - first, kGroupRows);
+    const int in = L % span;
+    tm = first + in % rows;
+    tn = in / rows;
+}
+
 // RECON: the low-rank reconstruction form (column scale on op(A), optional
 // minuend), instantiated separately so the power-iteration GEMMs carry no
 // epilogue branches and profiles tell the two apart.
@@ -181,7 +203,9 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int tile_m, tile_n;
+    xcd_tile(blockIdx.x, ceil_div(g.M, BM), ceil_div(g.N, BN), tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
     const int kbeg = blockIdx.z * g.k_per_split;
     const int kend = min(g.K, kbeg + g.k_per_split);
 
@@ -395,7 +419,7 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
         g.ldc = ldc;
         g.split_stride = 0;
     }
-    dim3 grid(static_cast<unsigned>(ceil_div(N, BN)), static_cast<unsigned>(ceil_div(M, BM)), splits);
+    dim3 grid(static_cast<unsigned>(ceil_div(N, BN) * ceil_div(M, BM)), 1, splits);
     const bool recon = a_colscale || minuend;
     if (recon) {
         BSQ_REQUIRE(!ta && tb, "gemm: column scale / minuend only in the A * B^T form");

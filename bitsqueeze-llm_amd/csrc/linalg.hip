@@ -458,6 +458,7 @@ __device__ void tridl_factor(const double *__restrict__ d, const double *__restr
                              double tiny, double *__restrict__ u0inv, double *__restrict__ u1,
                              double *__restrict__ u2, double *__restrict__ ml, int *__restrict__ piv, int st) {
     double dcur = d[0] - lam, ecur = (k > 1) ? e[0] : 0.0;
+    const double inv_tiny = 1.0 / tiny;
 #pragma unroll 4
     for (int i = 0; i < k - 1; ++i) {
         const double sub = e[i];                        // T[i+1][i]
@@ -473,7 +474,9 @@ __device__ void tridl_factor(const double *__restrict__ d, const double *__restr
         const double m = (keep ? sub : dcur) * rp;
         piv[i * st] = keep ? 0 : 1;
         ml[i * st] = m;
-        u0inv[i * st] = 1.0 / ((fabs(p) < tiny) ? (p < 0.0 ? -tiny : tiny) : p);
+        // the refined reciprocal serves the backward pass too (pivots below
+        // tiny are replaced by +-tiny there, as in the division it stands for)
+        u0inv[i * st] = (fabs(p) < tiny) ? (p < 0.0 ? -inv_tiny : inv_tiny) : rp;
         u1[i * st] = keep ? ecur : dn;
         u2[i * st] = keep ? 0.0 : en;
         const double ndcur = keep ? fma(-m, ecur, dn) : fma(-m, dn, ecur);
@@ -642,16 +645,24 @@ __global__ void backtransform_kernel(const double *__restrict__ W, const double 
     for (int i = lane; i < k; i += 64) Uh[static_cast<uint64_t>(i) * k + t] = static_cast<float>(z[i]);
 }
 
-// Bisection by multisection: one wave per eigenvalue, 63 interior points per
-// pass.  lambda[t] = t-th largest eigenvalue.
-__global__ __launch_bounds__(64) void multisect_kernel(const double *__restrict__ d, const double *__restrict__ e,
-                                                        int k, double *__restrict__ lambda, double *__restrict__ tnorm_out) {
+// Bisection by multisection: one workgroup of kMsThreads lanes per
+// eigenvalue, kMsThreads - 1 interior points per pass (8 bits of the
+// interval per pass with 256 lanes).  Each Sturm count is a sequential
+// recurrence, so a pass costs one count's latency however many lanes share
+// it, and more lanes mean fewer passes.  lambda[t] = t-th largest eigenvalue.
+constexpr int kMsThreads = 256;
+__global__ __launch_bounds__(kMsThreads) void multisect_kernel(const double *__restrict__ d,
+                                                               const double *__restrict__ e, int k,
+                                                               double *__restrict__ lambda,
+                                                               double *__restrict__ tnorm_out) {
     extern __shared__ double sm[];  // d[k], e2[k]
     double *sd = sm, *se2 = sm + k;
-    __shared__ double bounds[2];
-    const int lane = threadIdx.x;
+    constexpr int W = kMsThreads / 64;
+    __shared__ double red[3][W];
+    __shared__ unsigned long long masks[W];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     double lo = 1e300, hi = -1e300, emax = 0.0;
-    for (int i = lane; i < k; i += 64) {
+    for (int i = tid; i < k; i += kMsThreads) {
         sd[i] = d[i];
         const double ei = (i + 1 < k) ? e[i] : 0.0;
         se2[i] = ei * ei;
@@ -665,7 +676,20 @@ __global__ __launch_bounds__(64) void multisect_kernel(const double *__restrict_
         hi = fmax(hi, __shfl_xor(hi, off));
         emax = fmax(emax, __shfl_xor(emax, off));
     }
+    if (lane == 0) {
+        red[0][wave] = lo;
+        red[1][wave] = hi;
+        red[2][wave] = emax;
+    }
     __syncthreads();
+    lo = red[0][0];
+    hi = red[1][0];
+    emax = red[2][0];
+    for (int w = 1; w < W; ++w) {
+        lo = fmin(lo, red[0][w]);
+        hi = fmax(hi, red[1][w]);
+        emax = fmax(emax, red[2][w]);
+    }
     const double tnorm = fmax(fabs(lo), fabs(hi));
     const double pivmin = DBL_MIN * fmax(1.0, emax) * 4.0;
     lo -= 2.0 * tnorm * DBL_EPSILON * k + pivmin;
@@ -674,23 +698,28 @@ __global__ __launch_bounds__(64) void multisect_kernel(const double *__restrict_
     const int target = k - 1 - t;  // ascending index of the wanted eigenvalue
     double a = lo, b = hi;
     // absolute tolerance k * eps * ||T|| (a backward-stable eigenvalue is not more
-    // accurate than that): with 64 points per pass that is <= 9 passes
+    // accurate than that)
     const double abstol = static_cast<double>(k) * DBL_EPSILON * tnorm + pivmin;
-    for (int pass = 0; pass < 40; ++pass) {
+    for (int pass = 0; pass < 40; ++pass) {  // a, b and the exits are uniform
         if (b - a <= 2.0 * DBL_EPSILON * fmax(fabs(a), fabs(b)) + abstol) break;
-        const double h = (b - a) / 64.0;
-        const double x = a + h * (lane + 1);  // lanes 0..62 interior, lane 63 = b
-        const int cnt = (lane < 63) ? sturm_count(sd, se2, k, x, pivmin) : k + 1;
+        const double h = (b - a) / static_cast<double>(kMsThreads);
+        const double x = a + h * (tid + 1);  // lanes 0..kMsThreads-2 interior, the last = b
+        const int cnt = (tid < kMsThreads - 1) ? sturm_count(sd, se2, k, x, pivmin) : k + 1;
         // smallest point whose count exceeds target bounds the eigenvalue from above
         const unsigned long long above = __ballot(cnt > target);
-        const int first = __ffsll(above) - 1;  // always found (lane 63)
+        __syncthreads();  // the previous pass's masks are read
+        if (lane == 0) masks[wave] = above;
+        __syncthreads();
+        int first = kMsThreads - 1;  // always found (the last lane)
+        for (int w = W - 1; w >= 0; --w)
+            if (masks[w]) first = w * 64 + __ffsll(masks[w]) - 1;
         const double nb = a + h * (first + 1);
         const double na = (first == 0) ? a : a + h * first;
         if (!(nb < b) && !(na > a)) break;
         a = na;
         b = fmin(nb, b);
     }
-    if (lane == 0) {
+    if (tid == 0) {
         lambda[t] = 0.5 * (a + b);
         if (t == 0 && tnorm_out) tnorm_out[0] = tnorm;
     }
@@ -832,7 +861,7 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
         sytrd_kernel<<<1, kBig, 2 * k * sizeof(double), stream>>>(W, k, d, e, tau);
     }
     BSQ_HIP(hipGetLastError());
-    multisect_kernel<<<k, 64, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);
+    multisect_kernel<<<k, kMsThreads, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);
     BSQ_HIP(hipGetLastError());
     // eigenvalues per workgroup whose LDS arrays fit: (6kP + 2k) doubles + kP ints
     const int64_t lds_cap = 160 * 1024;
