@@ -19,6 +19,10 @@
 //                         FP32 row-major (B[r][c] = L^{-1}[c][r]) so that the
 //                         orthonormal basis is the plain product Q = X B.
 //
+//   ns_refine_kernel      the final basis's second pass: one Newton-Schulz
+//                         step instead of a second Cholesky when the basis is
+//                         already orthonormal to working accuracy (below).
+//
 // The reference orthonormalises with Householder QR (cuSOLVER geqrf/orgqr,
 // modules/svd_lowrank_cuda/src/svd_lowrank_cuda.cu:250-282); any basis of the
 // same column space serves the range finder.
@@ -87,7 +91,9 @@ template <int NB>
 __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double *__restrict__ G, int k,
                                                                      double *__restrict__ Lout,
                                                                      double *__restrict__ LIout,
-                                                                     int *__restrict__ status) {
+                                                                     int *__restrict__ status,
+                                                                     const int *__restrict__ run) {
+    if (run && run[0] == 0) return;  // uniform: the refinement step replaced this pass
     constexpr int KP = NB * 32, NE = NB * (NB + 1) / 2, PR = (NB > 1) ? (NB - 1) * 32 : 1;
     __shared__ double Dg[32][33];                          // diagonal block (row-major)
     __shared__ double LT[32][33];                          // L_jj column-major: LT[s][t] = L[t][s]
@@ -276,7 +282,8 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
 // Output B = L^{-T} (k x k FP32 row-major): B[c][r] = L^{-1}[r][c].
 template <int NB>
 __global__ __launch_bounds__(256) void trinv_kernel(const double *__restrict__ Lin, const double *__restrict__ LIin,
-                                                    int k, float *__restrict__ B) {
+                                                    int k, float *__restrict__ B, const int *__restrict__ run) {
+    if (run && run[0] == 0) return;  // uniform
     constexpr int KP = NB * 32;
     __shared__ double X[KP][8];
     __shared__ double S[32][8];
@@ -308,12 +315,42 @@ __global__ __launch_bounds__(256) void trinv_kernel(const double *__restrict__ L
 }
 
 template <int NB>
-void chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream) {
+void chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, const int *run, hipStream_t stream) {
     double *L = Lbuf, *LI = Lbuf + static_cast<uint64_t>(NB) * 32 * NB * 32;
-    chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, status);
+    chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, status, run);
     BSQ_HIP(hipGetLastError());
-    trinv_kernel<NB><<<static_cast<unsigned>(ceil_div(k, 8)), 256, 0, stream>>>(L, LI, k, B);
+    trinv_kernel<NB><<<static_cast<unsigned>(ceil_div(k, 8)), 256, 0, stream>>>(L, LI, k, B, run);
     BSQ_HIP(hipGetLastError());
+}
+
+// Second pass over an almost orthonormal basis Q with G = Q^T Q = I + E.
+// When ||E||_F < kNsTol, B = 1.5 I - 0.5 G and Q B has orthogonality error
+// O(||E||^2) (one Newton-Schulz step towards the polar factor; the column
+// space is unchanged, B being nonsingular), which is what a second CholeskyQR
+// pass achieves at the cost of a one-CU factorisation.  run[0] = 0 then, and
+// the Cholesky kernels launched behind this one return at once; otherwise
+// run[0] = 1, B is left alone and they compute B = L^{-T} as usual.
+constexpr double kNsTol = 1e-3;
+// One workgroup per row of B.  rowsq[r] is row r's share of ||E||_F^2
+// (written by the Gram reduction); every workgroup sums the k shares in the
+// same order, so all of them reach the same decision.
+__global__ __launch_bounds__(256) void ns_refine_kernel(const double *__restrict__ G,
+                                                        const double *__restrict__ rowsq, int k,
+                                                        float *__restrict__ B, int *__restrict__ run) {
+    __shared__ double red[4];
+    const int tid = threadIdx.x, i = blockIdx.x;
+    double s = (tid < k) ? rowsq[tid] : 0.0;  // k <= 256
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const bool refine = tot < kNsTol * kNsTol;  // false for NaN
+    if (i == 0 && tid == 0) run[0] = refine ? 0 : 1;
+    if (!refine) return;
+    for (int j = tid; j < k; j += 256) {
+        const uint64_t t = static_cast<uint64_t>(i) * k + j;
+        B[t] = static_cast<float>((i == j ? 1.5 : 0.0) - 0.5 * G[t]);
+    }
 }
 
 }  // namespace
@@ -328,18 +365,31 @@ bool chol_blocked_supported(int k) { return k >= 1 && k <= 256; }
 
 // G = L L^T (with shifted restarts on breakdown) and B = L^{-T} (FP32,
 // k x k row-major), so that X B has orthonormal columns when G = X^T X.
-void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream) {
+void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream,
+                         const int *run) {
     BSQ_REQUIRE(chol_blocked_supported(k), "chol: rank outside the blocked kernel's range");
     switch (ceil_div(k, 32)) {
-        case 1: chol_blocked<1>(G, k, Lbuf, B, status, stream); break;
-        case 2: chol_blocked<2>(G, k, Lbuf, B, status, stream); break;
-        case 3: chol_blocked<3>(G, k, Lbuf, B, status, stream); break;
-        case 4: chol_blocked<4>(G, k, Lbuf, B, status, stream); break;
-        case 5: chol_blocked<5>(G, k, Lbuf, B, status, stream); break;
-        case 6: chol_blocked<6>(G, k, Lbuf, B, status, stream); break;
-        case 7: chol_blocked<7>(G, k, Lbuf, B, status, stream); break;
-        default: chol_blocked<8>(G, k, Lbuf, B, status, stream); break;
+        case 1: chol_blocked<1>(G, k, Lbuf, B, status, run, stream); break;
+        case 2: chol_blocked<2>(G, k, Lbuf, B, status, run, stream); break;
+        case 3: chol_blocked<3>(G, k, Lbuf, B, status, run, stream); break;
+        case 4: chol_blocked<4>(G, k, Lbuf, B, status, run, stream); break;
+        case 5: chol_blocked<5>(G, k, Lbuf, B, status, run, stream); break;
+        case 6: chol_blocked<6>(G, k, Lbuf, B, status, run, stream); break;
+        case 7: chol_blocked<7>(G, k, Lbuf, B, status, run, stream); break;
+        default: chol_blocked<8>(G, k, Lbuf, B, status, run, stream); break;
     }
+}
+
+// B such that Q B is orthonormal for the almost orthonormal Q with Gram G
+// (and row shares rowsq of ||G - I||_F^2): the Newton-Schulz step when it
+// suffices, else B = L^{-T} from a Cholesky factorisation (decided on the
+// device; run is one int of scratch).
+void launch_orth_refine(const double *G, const double *rowsq, int k, double *Lbuf, float *B, int *status, int *run,
+                        hipStream_t stream) {
+    BSQ_REQUIRE(k >= 1 && k <= 256, "orth refine: rank outside the blocked kernels' range");
+    ns_refine_kernel<<<static_cast<unsigned>(k), 256, 0, stream>>>(G, rowsq, k, B, run);
+    BSQ_HIP(hipGetLastError());
+    launch_chol_blocked(G, k, Lbuf, B, status, stream, run);
 }
 
 }  // namespace bsq

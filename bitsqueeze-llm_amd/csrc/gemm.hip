@@ -346,14 +346,23 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
 // C[i, j] = sum_z W[z][i, j] in a fixed order.
 __global__ void splitk_reduce_kernel(const float *__restrict__ W, int splits, uint64_t stride, int M, int N,
                                      int ldc, float *__restrict__ C) {
-    const uint64_t total = static_cast<uint64_t>(M) * N;
-    for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
-         t += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-        const uint64_t i = t / N, j = t % N;
-        float s = W[t];
-        for (int z = 1; z < splits; ++z) s += W[z * stride + t];
-        C[i * ldc + j] = s;
-    }
+    // rows by grid-stride, columns by lane: no 64-bit division per element
+    for (int i = blockIdx.y; i < M; i += gridDim.y)
+        for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < N; j += gridDim.x * blockDim.x) {
+            const uint64_t t = static_cast<uint64_t>(i) * N + j;
+            // the partials' loads are issued eight at a time, summed in split order
+            float s = W[t];
+            int z = 1;
+            for (; z + 8 <= splits; z += 8) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = W[(z + u) * stride + t];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += v[u];
+            }
+            for (; z < splits; ++z) s += W[z * stride + t];
+            C[static_cast<uint64_t>(i) * ldc + j] = s;
+        }
 }
 
 // Split count minimising the modelled time: rounds of resident workgroups
@@ -430,12 +439,9 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
     else gemm_mfma_kernel<true, true, false><<<grid, kThreads, 0, stream>>>(g);
     BSQ_HIP(hipGetLastError());
     if (splits > 1) {
-        const uint64_t total = static_cast<uint64_t>(M) * N;
-        uint64_t rgrid = ceil_div(total, 256);
-        const uint64_t cap = static_cast<uint64_t>(cu_count()) * 8;
-        if (rgrid > cap) rgrid = cap;
-        splitk_reduce_kernel<<<static_cast<unsigned>(rgrid), 256, 0, stream>>>(workspace, splits, g.split_stride, M,
-                                                                              N, ldc, C);
+        const dim3 rgrid(static_cast<unsigned>(ceil_div(N, 256)),
+                         static_cast<unsigned>(std::min<uint64_t>(M, static_cast<uint64_t>(cu_count()) * 8)));
+        splitk_reduce_kernel<<<rgrid, 256, 0, stream>>>(workspace, splits, g.split_stride, M, N, ldc, C);
         BSQ_HIP(hipGetLastError());
     }
 }

@@ -132,16 +132,41 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
 }
 
 // G[i][j] = G[j][i] = sum_s P[s][i][j] (lower entries), fixed order.
-__global__ void gram_reduce_kernel(const double *__restrict__ P, int splits, int k, double *__restrict__ G) {
+// One row per workgroup (grid-stride), columns by lane.  With rowsq,
+// rowsq[i] = sum over row i of the full symmetric G of (G - I)^2 (the
+// squared Frobenius distance from I, split by rows, summed in a fixed order).
+__global__ __launch_bounds__(256) void gram_reduce_kernel(const double *__restrict__ P, int splits, int k,
+                                                          double *__restrict__ G, double *__restrict__ rowsq) {
+    __shared__ double red[4];
     const uint64_t kk = static_cast<uint64_t>(k) * k;
-    for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < kk;
-         t += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-        const int i = static_cast<int>(t / k), j = static_cast<int>(t % k);
-        if (j > i) continue;
-        double s = 0.0;
-        for (int z = 0; z < splits; ++z) s += P[z * kk + t];
-        G[t] = s;
-        G[static_cast<uint64_t>(j) * k + i] = s;
+    for (int i = blockIdx.x; i < k; i += gridDim.x) {  // uniform per workgroup
+        double sq = 0.0;
+        for (int j = threadIdx.x; j <= i; j += blockDim.x) {
+            const uint64_t t = static_cast<uint64_t>(i) * k + j;
+            // the partials' loads are issued eight at a time, summed in split order
+            double s = 0.0;
+            int z = 0;
+            for (; z + 8 <= splits; z += 8) {
+                double v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = P[(z + u) * kk + t];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += v[u];
+            }
+            for (; z < splits; ++z) s += P[z * kk + t];
+            G[t] = s;
+            G[static_cast<uint64_t>(j) * k + i] = s;
+            // row i of the full matrix: the lower entries here, the upper ones
+            // mirrored from the rows below, so off-diagonal squares count twice
+            sq += (j == i) ? (s - 1.0) * (s - 1.0) : 2.0 * s * s;
+        }
+        if (rowsq) {
+            for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+            __syncthreads();
+            if (threadIdx.x == 0) rowsq[i] = (red[0] + red[1]) + (red[2] + red[3]);
+            __syncthreads();
+        }
     }
 }
 
@@ -821,7 +846,8 @@ uint64_t gram_workspace_bytes(int M, int k) {
     return static_cast<uint64_t>(gram_splits(M, k)) * k * k * sizeof(double);
 }
 
-void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream) {
+void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream,
+                 double *rowsq) {
     const int nt = static_cast<int>(ceil_div(k, kGramTile));
     const int tiles = nt * (nt + 1) / 2;
     int splits = gram_splits(M, k);
@@ -830,9 +856,7 @@ void launch_gram(const float *X, int M, int k, int ld, double *G, double *worksp
     const bool vec = (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15u) == 0);
     gram_mfma_kernel<<<dim3(tiles, splits), 256, 0, stream>>>(X, M, k, ld, rows_per, vec, workspace);
     BSQ_HIP(hipGetLastError());
-    const uint64_t kk = static_cast<uint64_t>(k) * k;
-    const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(ceil_div(kk, 256), 1024));
-    gram_reduce_kernel<<<grid, 256, 0, stream>>>(workspace, splits, k, G);
+    gram_reduce_kernel<<<static_cast<unsigned>(k), 256, 0, stream>>>(workspace, splits, k, G, rowsq);
     BSQ_HIP(hipGetLastError());
 }
 

@@ -27,11 +27,15 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
                  int ldc, const float *a_colscale, const float *minuend, float *workspace, uint64_t workspace_bytes,
                  hipStream_t stream);
 uint64_t gram_workspace_bytes(int M, int k);
-void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream);
+void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream,
+                 double *rowsq = nullptr);
 void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream);
 uint64_t chol_blocked_buffer_doubles(int k);
 bool chol_blocked_supported(int k);
-void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream);
+void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream,
+                         const int *run = nullptr);
+void launch_orth_refine(const double *G, const double *rowsq, int k, double *Lbuf, float *B, int *status, int *run,
+                        hipStream_t stream);
 void launch_syev(const double *G, int k, double *W, double *Z, double *small, double *scratch, int *iscratch,
                  double *lambda, float *Uh, hipStream_t stream);
 
@@ -187,6 +191,7 @@ struct SvdPlan {
     float *cbest = nullptr, *csign = nullptr;  // column statistics of the final normalisation
     int *cidx = nullptr;
     double *csum = nullptr;
+    double *rowsq = nullptr;  // per-row squared distance of the final Gram from I
     int *iscratch = nullptr, *status = nullptr;
     double *gram_ws = nullptr;
     float *gemm_ws = nullptr;
@@ -207,6 +212,7 @@ struct SvdPlan {
         release(csign);
         release(cidx);
         release(csum);
+        release(rowsq);
         release(Z);
         release(small);
         release(scratch);
@@ -246,6 +252,7 @@ SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
         p->cbest = alloc<float>(kColChunks * k);
         p->cidx = alloc<int>(kColChunks * k);
         p->csum = alloc<double>(kColChunks * k);
+        p->rowsq = alloc<double>(k);
         p->csign = alloc<float>(2 * k);
         p->scratch = alloc<double>(9 * k * k);
         p->lambda = alloc<double>(k);
@@ -317,8 +324,16 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
         orth(Xa, Xb, Mw);
         std::swap(Xa, Xb);
     }
-    // second CholeskyQR pass on the final basis (CholeskyQR2)
-    orth(Xa, Xb, Mw);
+    // second pass on the final basis: CholeskyQR2, or, when the first pass
+    // left it orthonormal to working accuracy, one Newton-Schulz step
+    if (p->Lbuf) {
+        launch_gram(Xa, Mw, k, k, p->G, p->gram_ws, st, p->rowsq);
+        launch_orth_refine(p->G, p->rowsq, k, p->Lbuf, p->Linv, p->status, p->status + 1, st);
+        launch_gemm(false, false, Mw, k, k, Xa, k, p->Linv, k, Xb, k, nullptr, nullptr, p->gemm_ws,
+                    p->gemm_ws_bytes, st);
+    } else {
+        orth(Xa, Xb, Mw);
+    }
     std::swap(Xa, Xb);
     // Y = A_w^T Q = B^T;  B B^T = Y^T Y = U_hat diag(S^2) U_hat^T
     awt_times(Xa, Ya);
