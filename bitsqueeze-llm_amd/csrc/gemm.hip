@@ -14,13 +14,15 @@
 // epilogue (error = residual - U S V^T).
 //
 // Tiling: 256 threads = 4 waves in a 2 x 2 grid; workgroup tile 128 x 128,
-// BK = 16, so the double-buffered tiles take ~40 KB of LDS and three or four
-// workgroups share a CU (more waves to cover each other's barrier and
-// global-load waits than the two that 32-deep tiles allow); each wave owns
-// 64 x 64 as 4 x 4 MFMA 16x16 blocks (64 AGPRs).  Tiles move global ->
-// registers (16-byte loads where the layout allows) -> LDS in their global
-// orientation (16-byte writes; layouts below) while the previous tile is
-// multiplied.  Skinny shapes are split
+// BK = 16; each wave owns 64 x 64 as 4 x 4 MFMA 16x16 blocks (64 AGPRs).
+// Two main loops share that tiling:
+//   gemm_dma_kernel   operand tiles go global -> LDS directly
+//                     (global_load_lds_dwordx4) through a ring of four
+//                     slices, three in flight while one is multiplied;
+//   gemm_mfma_kernel  the fallback for shapes the DMA layout does not take
+//                     (K not a multiple of 16, unaligned operands): tiles move
+//                     global -> registers -> LDS one slice ahead.
+// Both use the same k order per lane, so their results are identical.  Skinny shapes are split
 // along K so the grid fills the 256 CUs several times over; partial products
 // go to a workspace summed in a fixed order, so results are deterministic.
 #include "bsq_internal.hpp"
@@ -343,6 +345,224 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
             }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined variant: operand tiles go global -> LDS directly
+// (global_load_lds_dwordx4, 16 bytes per lane, no VGPR staging) through a
+// ring of kStages slices, so kStages - 1 slices are in flight while one is
+// multiplied.  Each wave-instruction fills one 1 KB LDS chunk, lane l at byte
+// 16 l, so the tile layouts are unpadded and XOR-swizzled at 16-byte
+// granularity to keep the fragment reads free of bank conflicts:
+//   k-contiguous tile (rows x 16 k): float index r*16 + 4*(q ^ f(r)) + e for
+//     k = 4q + e, f(r) = (r >> 1) & 3;
+//   k-major tile (16 k x 128 cols): float index kr*128 + (c ^ 16*((kr >> 2) & 1)).
+// Requires K % BK == 0, 16-byte aligned bases and leading dimensions, and
+// the k-major extents (M for TA, N for !TB) a multiple of 4 (rows beyond the
+// matrix are clamped to its last row or quad: their outputs are discarded).
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+constexpr int kStages = 4;
+constexpr int kTileF = 128 * BK;              // floats per operand tile (8 KB)
+constexpr int kStageF = 2 * kTileF;           // A + B
+constexpr int kDmaReconMaxK = 1024;           // RECON column scales staged in LDS
+
+__device__ __forceinline__ void dma16(const float *g, const float *l) {
+    __builtin_amdgcn_global_load_lds((glb_void_t *)(g), (lds_void_t *)(reinterpret_cast<size_t>(l)), 16, 0, 0);
+}
+// wave-level LDS barrier that does not drain the DMA queue: waits for this
+// wave's DMAs down to `pending` outstanding, then the workgroup barrier; the
+// asm statements keep the compiler from moving LDS accesses across it
+template <int PENDING>
+__device__ __forceinline__ void dma_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xF70 | PENDING);  // vmcnt(PENDING), expcnt/lgkmcnt untouched
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// one 1 KB chunk c (0..7) of a 128 x 16 tile
+template <bool KMAJOR>
+__device__ __forceinline__ void dma_chunk(const float *__restrict__ P, int ld, int r0, int extent, int k0, int c,
+                                          const float *lds_tile) {
+    const int l = threadIdx.x & 63;
+    if constexpr (!KMAJOR) {  // P row-major [row][k]
+        const int r = 16 * c + (l >> 2);
+        const int q = (l & 3) ^ ((r >> 1) & 3);
+        const int gr = min(r0 + r, extent - 1);
+        dma16(P + static_cast<uint64_t>(gr) * ld + k0 + 4 * q, lds_tile + c * 256);
+    } else {  // P row-major [k][col]
+        const int kr = 2 * c + (l >> 5);
+        const int cq = (l & 31) ^ (4 * ((kr >> 2) & 1));
+        const int gc = min(r0 + 4 * cq, extent - 4);
+        dma16(P + static_cast<uint64_t>(k0 + kr) * ld + gc, lds_tile + c * 256);
+    }
+}
+
+template <bool KMAJOR>
+__device__ __forceinline__ void dma_frag(const float *S, int row, int kk, float (&o)[KS]) {
+    if constexpr (!KMAJOR) {
+        const float4 v = *reinterpret_cast<const float4 *>(&S[row * 16 + 4 * (kk ^ ((row >> 1) & 3))]);
+        o[0] = v.x;
+        o[1] = v.y;
+        o[2] = v.z;
+        o[3] = v.w;
+    } else {
+        const int sw = 16 * (kk & 1);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) o[s] = S[(4 * kk + s) * 128 + (row ^ sw)];
+    }
+}
+
+template <bool TA, bool TB, bool RECON>
+__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    // one LDS object per stage: the compiler's wait insertion then sees that a
+    // DMA into one stage cannot alias the fragment reads of another
+    __shared__ __attribute__((aligned(1024))) float st0[kStageF];
+    __shared__ __attribute__((aligned(1024))) float st1[kStageF];
+    __shared__ __attribute__((aligned(1024))) float st2[kStageF];
+    __shared__ __attribute__((aligned(1024))) float st3[kStageF];
+    __shared__ float scs[RECON ? kDmaReconMaxK : 1];  // RECON: the column scales of op(A)
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    int tile_m, tile_n;
+    xcd_tile(blockIdx.x, ceil_div(g.M, BM), ceil_div(g.N, BN), tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int kbeg = blockIdx.z * g.k_per_split;
+    const int kend = min(g.K, kbeg + g.k_per_split);
+    const int nk = (kend - kbeg) / BK;
+
+    f32x4v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+    if constexpr (RECON) {
+        for (int t = tid; t < kend - kbeg; t += kThreads) scs[t] = g.a_colscale ? g.a_colscale[kbeg + t] : 1.0f;
+        // visible after the first barrier of the loop
+    }
+    // each wave issues chunks 2w, 2w+1 of A and of B: four DMAs per slice
+    auto issue = [&](const float *st, int j) {
+        const int k0 = kbeg + j * BK;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c = 2 * wave + h;
+            dma_chunk<TA>(g.A, g.lda, m0, g.M, k0, c, st);
+            dma_chunk<!TB>(g.B, g.ldb, n0, g.N, k0, c, st + kTileF);
+        }
+    };
+    const int kk = lane >> 4, cc = lane & 15;
+    // slice j sits in stage j % 4: cur holds it, nxt (= stage (j + 3) % 4, read
+    // in iteration j - 1) receives slice j + 3
+    auto body = [&](const float *cur, const float *nxt, int j) {
+        const int ahead = min(kStages - 2, nk - 1 - j);  // slices issued after j
+        if (ahead >= 2) dma_barrier<8>();
+        else if (ahead == 1) dma_barrier<4>();
+        else dma_barrier<0>();
+        if (j + kStages - 1 < nk) issue(nxt, j + kStages - 1);
+        float a[FM][KS], b[FN][KS];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) dma_frag<TA>(cur, wm0 + i * 16 + cc, kk, a[i]);
+        if constexpr (RECON) {
+#pragma unroll
+            for (int s2 = 0; s2 < KS; ++s2) {
+                const float sc = scs[j * BK + KS * kk + s2];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) a[i][s2] *= sc;
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < FN; ++jj) dma_frag<!TB>(cur + kTileF, wn0 + jj * 16 + cc, kk, b[jj]);
+#pragma unroll
+        for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int jj = 0; jj < FN; ++jj)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s2], b[jj][s2], acc[i][jj], 0, 0, 0);
+    };
+    if (0 < nk) issue(st0, 0);
+    if (1 < nk) issue(st1, 1);
+    if (2 < nk) issue(st2, 2);
+    for (int j = 0; j < nk; j += kStages) {
+        body(st0, st3, j);
+        if (j + 1 < nk) body(st1, st0, j + 1);
+        if (j + 2 < nk) body(st2, st1, j + 2);
+        if (j + 3 < nk) body(st3, st2, j + 3);
+    }
+
+    float *C = g.C + static_cast<uint64_t>(blockIdx.z) * g.split_stride;
+    // fragment (i, j) register r holds row 4*(lane/16) + r, column lane % 16
+    if constexpr (RECON) {
+        // the output tile leaves through stage 0 in four 32-row passes so that
+        // rows go out as 16-byte stores and the minuend comes in as 16-byte
+        // loads; columns are XOR-swizzled by 16 on alternate groups of four
+        // rows (the fragment writes of rows r and r + 4 then hit disjoint banks)
+        float *Cs = st0;
+        const bool vec_c = ((g.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15u) == 0) &&
+                           (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
+        constexpr int Q = 32 * BN / 4 / kThreads;  // float4 per thread per pass
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            float4 mv[Q];
+            if (g.minuend && vec_c) {
+#pragma unroll
+                for (int q = 0; q < Q; ++q) {
+                    const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
+                    const int gi = m0 + 32 * p + rr, gj = n0 + 4 * c4;
+                    mv[q] = (gi < g.M && gj + 4 <= g.N)
+                                ? *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj)
+                                : float4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+            __syncthreads();  // the ring (p = 0) or the previous pass is consumed
+            if (wm0 == 64 * (p / 2)) {
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int rl = 16 * ii + 4 * (lane >> 4) + r;
+                            const int col = wn0 + j * 16 + (lane & 15);
+                            Cs[rl * BN + (col ^ (16 * ((rl >> 2) & 1)))] = acc[2 * (p % 2) + ii][j][r];
+                        }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
+                const int gi = m0 + 32 * p + rr, gj = n0 + 4 * c4;
+                if (gi >= g.M) continue;
+                float4 v = *reinterpret_cast<const float4 *>(&Cs[rr * BN + ((4 * c4) ^ (16 * ((rr >> 2) & 1)))]);
+                const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
+                if (vec_c && gj + 4 <= g.N) {
+                    if (g.minuend) v = float4{mv[q].x - v.x, mv[q].y - v.y, mv[q].z - v.z, mv[q].w - v.w};
+                    *reinterpret_cast<float4 *>(C + e) = v;
+                } else {
+                    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (gj + u < g.N) C[e + u] = g.minuend ? g.minuend[e + u] - vv[u] : vv[u];
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gi = m0 + wm0 + i * 16 + 4 * (lane >> 4) + r;
+                const int gj = n0 + wn0 + j * 16 + (lane & 15);
+                if (gi < g.M && gj < g.N) C[static_cast<uint64_t>(gi) * g.ldc + gj] = acc[i][j][r];
+            }
+}
+
 // C[i, j] = sum_z W[z][i, j] in a fixed order.
 __global__ void splitk_reduce_kernel(const float *__restrict__ W, int splits, uint64_t stride, int M, int N,
                                      int ldc, float *__restrict__ C) {
@@ -430,7 +650,19 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
     }
     dim3 grid(static_cast<unsigned>(ceil_div(N, BN) * ceil_div(M, BM)), 1, splits);
     const bool recon = a_colscale || minuend;
-    if (recon) {
+    // the DMA-pipelined kernel wherever its layout constraints hold, else the
+    // register-staged one
+    const bool dma = g.vec_a && g.vec_b && (K % BK == 0) && (!ta || M % 4 == 0) &&
+                     (tb || N % 4 == 0) && (!recon || K <= kDmaReconMaxK);
+    if (dma) {
+        if (recon) {
+            BSQ_REQUIRE(!ta && tb, "gemm: column scale / minuend only in the A * B^T form");
+            gemm_dma_kernel<false, true, true><<<grid, kThreads, 0, stream>>>(g);
+        } else if (!ta && !tb) gemm_dma_kernel<false, false, false><<<grid, kThreads, 0, stream>>>(g);
+        else if (ta && !tb) gemm_dma_kernel<true, false, false><<<grid, kThreads, 0, stream>>>(g);
+        else if (!ta && tb) gemm_dma_kernel<false, true, false><<<grid, kThreads, 0, stream>>>(g);
+        else gemm_dma_kernel<true, true, false><<<grid, kThreads, 0, stream>>>(g);
+    } else if (recon) {
         BSQ_REQUIRE(!ta && tb, "gemm: column scale / minuend only in the A * B^T form");
         gemm_mfma_kernel<false, true, true><<<grid, kThreads, 0, stream>>>(g);
     } else if (!ta && !tb) gemm_mfma_kernel<false, false, false><<<grid, kThreads, 0, stream>>>(g);
