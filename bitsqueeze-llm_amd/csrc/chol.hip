@@ -96,11 +96,9 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
     if (run && run[0] == 0) return;  // uniform: the refinement step replaced this pass
     constexpr int KP = NB * 32, NE = NB * (NB + 1) / 2, PR = (NB > 1) ? (NB - 1) * 32 : 1;
     __shared__ double Dg[32][33];                          // diagonal block (row-major)
-    __shared__ double LT[32][33];                          // L_jj column-major: LT[s][t] = L[t][s]
     __shared__ __attribute__((aligned(16))) double LI[32][34];  // L_jj^{-1}, row-major
     __shared__ __attribute__((aligned(16))) double P[PR][34];   // panel rows below the diagonal block
     __shared__ double stash[NE][64];                       // wave 0's registers during its solo phase
-    __shared__ double colb[32];                            // column broadcast of the 32 x 32 factorisation
     __shared__ double red[kCholThreads / 64];
     __shared__ int broke;
 

@@ -585,22 +585,24 @@ __global__ void splitk_reduce_kernel(const float *__restrict__ W, int splits, ui
         }
 }
 
-// Split count minimising the modelled time: rounds of resident workgroups
-// (three 128x128 tiles fit one CU's LDS) times the K slice each one walks,
-// plus the traffic of summing the partials.
+// Split count minimising the modelled time.  Measured on gfx950, a CU works
+// through ~1 slice of one 128 x 128 x 16 tile per 1.1 us when it holds two
+// or more workgroups (1.2 us with one), so the time is the busiest CU's share:
+// ceil(workgroups / CUs) x slices per workgroup x 1.1 us, plus, with splits,
+// the fixed-order reduce (~5 us of launch and latency plus its bytes at
+// ~5 TB/s).  Fits the power-iteration shapes to within ~7 %.
 int choose_splits(int M, int N, int K) {
     const uint64_t tiles = ceil_div(M, BM) * ceil_div(N, BN);
-    const uint64_t slots = static_cast<uint64_t>(cu_count()) * 3;
+    const uint64_t cus = static_cast<uint64_t>(cu_count());
     const uint64_t ksteps = ceil_div(K, BK);
     double best = 0.0;
     int best_s = 1;
     for (int s = 1; s <= 32; ++s) {
-        if (s > 1 && ksteps * BK / s < 256) break;  // keep >= 256 K values per split
-        const uint64_t rounds = ceil_div(tiles * s, slots);
-        // one K step of a 128x128xBK tile ~ 2 * 128 * 128 * BK / (256 flop/clk) cycles;
-        // the reduce moves (s + 1) * M * N * 4 bytes at ~ 2 KB / clk chip-wide.
-        const double t = static_cast<double>(rounds) * ceil_div(ksteps, s) * (128.0 * BK) +
-                         (s > 1 ? (s + 1.0) * M * N * 4.0 / 2048.0 : 0.0);
+        if (s > 1 && ksteps / s < 16) break;  // keep >= 16 slices per split (short K: no split)
+        const uint64_t per_cu = ceil_div(tiles * s, cus);
+        const double step_us = per_cu >= 2 ? 1.1 : 1.2;  // one workgroup alone hides less latency
+        const double t = static_cast<double>(per_cu) * ceil_div(ksteps, s) * step_us +
+                         (s > 1 ? 5.0 + (s + 1.0) * M * N * 4.0 / 5e6 : 0.0);
         if (s == 1 || t < best) {
             best = t;
             best_s = s;
