@@ -113,18 +113,21 @@ __global__ __launch_bounds__(kTrdThreads) void sytrd_blocked_kernel(const double
             // counts for its row when tx <= ty and for its column when tx < ty.
             const double mrow = static_cast<double>(1u - (static_cast<unsigned>(ty - tx) >> 31));
             const double mcol = static_cast<double>(static_cast<unsigned>(tx - ty) >> 31);
-            double va[NB];
+            // v at this lane's row and column indices, kept in registers for the
+            // update below (which then reads mostly w from LDS: LDS bytes per
+            // step bound this kernel)
+            double va[NB], vb[NB];
 #pragma unroll
-            for (int a = jb; a < NB; ++a) va[a] = vs[a * 32 + ty];
+            for (int a = jb; a < NB; ++a) {
+                va[a] = vs[a * 32 + ty];
+                vb[a] = vs[a * 32 + tx];
+            }
             double quad = 0.0;
 #pragma unroll
             for (int a = jb; a < NB; ++a) {
                 double rowp = 0.0;
 #pragma unroll
-                for (int b = jb; b <= a; ++b) {
-                    const double vb = vs[b * 32 + tx];
-                    rowp = fma(r[tri(a, b)], (a == b) ? vb * mrow : vb, rowp);
-                }
+                for (int b = jb; b <= a; ++b) rowp = fma(r[tri(a, b)], (a == b) ? vb[b] * mrow : vb[b], rowp);
                 PP[a][ty][tx] = rowp;
                 quad = fma(rowp, va[a], quad);
             }
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(kTrdThreads) void sytrd_blocked_kernel(const double
 #pragma unroll
                 for (int a = b; a < NB; ++a) colp = fma(r[tri(a, b)], (a == b) ? va[a] * mcol : va[a], colp);
                 PP[b][tx][32 + ty] = colp;
-                quad = fma(colp, vs[b * 32 + tx], quad);
+                quad = fma(colp, vb[b], quad);
             }
             quad = wave_sum_dpp(quad);
             if (lane == 0) red[wave] = quad;
@@ -165,10 +168,12 @@ __global__ __launch_bounds__(kTrdThreads) void sytrd_blocked_kernel(const double
             // 4. A -= v w^T + w v^T (v and w vanish at indices <= j)
 #pragma unroll
             for (int a = jb; a < NB; ++a) {
-                const double v_a = vs[a * 32 + ty], w_a = ws[a * 32 + ty];
+                // at NB = 8 the row values are read again instead (holding both
+                // vectors through the finish phase spills there)
+                const double w_a = ws[a * 32 + ty], v_a = (NB < 8) ? va[a] : vs[a * 32 + ty];
 #pragma unroll
                 for (int b = jb; b <= a; ++b)
-                    r[tri(a, b)] = fma(-v_a, ws[b * 32 + tx], fma(-w_a, vs[b * 32 + tx], r[tri(a, b)]));
+                    r[tri(a, b)] = fma(-v_a, ws[b * 32 + tx], fma(-w_a, vb[b], r[tri(a, b)]));
             }
         }
     }

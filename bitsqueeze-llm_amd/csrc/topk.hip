@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
             // 16-byte loads, several in flight per lane: the row is read once
             const float4 *src4 = reinterpret_cast<const float4 *>(a.a + row0);
             float4 *cache4 = reinterpret_cast<float4 *>(cache);
-#pragma unroll 4
+#pragma unroll 8
             for (uint32_t c4 = threadIdx.x; c4 < cols / 4; c4 += kThreads) {
                 const float4 v4 = src4[c4];
                 cache4[c4] = v4;
@@ -203,27 +203,30 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
             // pairs of lanes when k allows: half the maxima to rank against
             const uint32_t nonempty = min(kThreads, groups);
             const bool pairs = 2 * k <= nonempty + 1 && k <= kThreads / 2;
-            unsigned long long gmax = tmax;
             if (pairs) {
                 const unsigned long long other = static_cast<unsigned long long>(static_cast<uint32_t>(
                     __builtin_amdgcn_update_dpp(0, static_cast<int>(tmax & 0xffffffffu), 0xB1, 0xF, 0xF, false))) |
                     (static_cast<unsigned long long>(static_cast<uint32_t>(
                         __builtin_amdgcn_update_dpp(0, static_cast<int>(tmax >> 32), 0xB1, 0xF, 0xF, false))) << 32);
-                gmax = other > tmax ? other : tmax;
-                if ((threadIdx.x & 1u) == 0) tm[threadIdx.x >> 1] = gmax;
+                if ((threadIdx.x & 1u) == 0) tm[threadIdx.x >> 1] = other > tmax ? other : tmax;
             } else {
                 tm[threadIdx.x] = tmax;
             }
             const uint32_t ng = pairs ? kThreads / 2 : kThreads;
             __syncthreads();
-            uint32_t above = 0;
-            const ulonglong2 *tm2 = reinterpret_cast<const ulonglong2 *>(tm);
-            for (uint32_t j = 0; j < ng / 2; ++j) {
-                const ulonglong2 t2 = tm2[j];
-                above += (t2.x > gmax ? 1u : 0u) + (t2.y > gmax ? 1u : 0u);
+            // group g's maximum is ranked by thread g alone (the first ng threads,
+            // whole waves), so every maximum is compared against the others once
+            if (threadIdx.x < ng) {
+                const unsigned long long gmax = tm[threadIdx.x];
+                uint32_t above = 0;
+                const ulonglong2 *tm2 = reinterpret_cast<const ulonglong2 *>(tm);
+                for (uint32_t j = 0; j < ng / 2; ++j) {
+                    const ulonglong2 t2 = tm2[j];
+                    above += (t2.x > gmax ? 1u : 0u) + (t2.y > gmax ? 1u : 0u);
+                }
+                // one group ranks k-1: the maxima of non-empty groups are distinct
+                if (above == k - 1) sh.kt = gmax;
             }
-            // one group ranks k-1: the maxima of non-empty groups are distinct
-            if (above == k - 1 && (!pairs || (threadIdx.x & 1u) == 0)) sh.kt = gmax;
             __syncthreads();
             const unsigned long long kt = sh.kt;
             // count with a bitmask of this lane's hits (<= 64 entries per lane)
