@@ -129,29 +129,38 @@ __global__ __launch_bounds__(256) void colstat_kernel(const float *__restrict__ 
     }
 }
 
-// Per column, in chunk order: the sign that makes the first largest-|.| entry
-// of U[:, t] non-negative, and 1 / ||Vh[:, t]|| (1 for a zero column).
-__global__ void colfinal_kernel(const float *__restrict__ U, int k, const float *__restrict__ pbest,
-                                const int *__restrict__ pidx, const double *__restrict__ psum,
-                                float *__restrict__ usign, float *__restrict__ vscale) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= k) return;
-    float best = -1.0f;
-    int bidx = 0x7FFFFFFF;
-    double s = 0.0;
-#pragma unroll 16
-    for (int c = 0; c < kColChunks; ++c) {
-        const float b = pbest[static_cast<uint64_t>(c) * k + t];
-        const int i = pidx[static_cast<uint64_t>(c) * k + t];
-        if (b > best || (b == best && i < bidx)) {
-            best = b;
-            bidx = i;
+// Per column (one wave, lane c holding chunk c's statistics): the sign that
+// makes the first largest-|.| entry of U[:, t] non-negative, and
+// 1 / ||Vh[:, t]|| (1 for a zero column).  The chunks combine by a butterfly:
+// largest value first, lowest index among equals; the squared norms by the
+// same fixed tree in every lane.
+__global__ __launch_bounds__(256) void colfinal_kernel(const float *__restrict__ U, int k,
+                                                       const float *__restrict__ pbest, const int *__restrict__ pidx,
+                                                       const double *__restrict__ psum, float *__restrict__ usign,
+                                                       float *__restrict__ vscale) {
+    static_assert(kColChunks == 64, "one lane per chunk");
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= k) return;  // whole waves
+    const uint64_t e = static_cast<uint64_t>(lane) * k + t;
+    float best = pbest[e];
+    int bidx = pidx[e];
+    double s = psum[e];
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ob = __shfl_xor(best, off);
+        const int oi = __shfl_xor(bidx, off);
+        const double os = __shfl_xor(s, off);
+        if (ob > best || (ob == best && oi < bidx)) {
+            best = ob;
+            bidx = oi;
         }
-        s += psum[static_cast<uint64_t>(c) * k + t];
+        s += os;
     }
-    const float sg = (bidx != 0x7FFFFFFF && U[static_cast<uint64_t>(bidx) * k + t] < 0.0f) ? -1.0f : 1.0f;
-    usign[t] = sg;
-    vscale[t] = (s > 0.0) ? sg * static_cast<float>(1.0 / sqrt(s)) : sg;
+    if (lane == 0) {
+        const float sg = (bidx != 0x7FFFFFFF && U[static_cast<uint64_t>(bidx) * k + t] < 0.0f) ? -1.0f : 1.0f;
+        usign[t] = sg;
+        vscale[t] = (s > 0.0) ? sg * static_cast<float>(1.0 / sqrt(s)) : sg;
+    }
 }
 
 // Uw[:, t] *= usign[t];  Vh[:, t] *= vscale[t]  (coalesced rows)
@@ -354,8 +363,8 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
     const float *Usrc = p->transposed ? Vh_out : Uw_out;  // U in the output orientation
     colstat_kernel<<<dim3(kColChunks, 2), 256, 0, st>>>(Usrc, m, Vh_out, Nw, k, p->cbest, p->cidx, p->csum);
     BSQ_HIP(hipGetLastError());
-    colfinal_kernel<<<static_cast<unsigned>(ceil_div(k, 256)), 256, 0, st>>>(Usrc, k, p->cbest, p->cidx, p->csum,
-                                                                             p->csign, p->csign + k);
+    colfinal_kernel<<<static_cast<unsigned>(ceil_div(k, 4)), 256, 0, st>>>(Usrc, k, p->cbest, p->cidx, p->csum,
+                                                                           p->csign, p->csign + k);
     BSQ_HIP(hipGetLastError());
     {
         const uint64_t nu = static_cast<uint64_t>(Mw) * k, nvh = static_cast<uint64_t>(Nw) * k;

@@ -645,14 +645,25 @@ bool try_launch_reg(const TopkArgs &a, hipStream_t stream) {
     return true;
 }
 
-__global__ void topk_scatter_kernel(const uint16_t *__restrict__ idx0, const float *__restrict__ val0, uint32_t k0,
-                                    const uint16_t *__restrict__ idx1, const float *__restrict__ val1, uint32_t k1,
-                                    uint32_t cols, float *__restrict__ dense, bool accumulate,
-                                    const uint32_t *__restrict__ gate0) {
+__global__ __launch_bounds__(256) void topk_scatter_kernel(const uint16_t *__restrict__ idx0,
+                                                           const float *__restrict__ val0, uint32_t k0,
+                                                           const uint16_t *__restrict__ idx1,
+                                                           const float *__restrict__ val1, uint32_t k1, uint32_t cols,
+                                                           float *__restrict__ dense, bool accumulate,
+                                                           const uint32_t *__restrict__ gate0) {
     const uint64_t r = blockIdx.x;
+    const uint32_t t = threadIdx.x, nt = blockDim.x;
     float *row = dense + r * cols;
+    // this thread's first entry of the second set, fetched before the first
+    // set's updates so its latency overlaps them
+    uint32_t c1 = 0xFFFFFFFFu;
+    float v1 = 0.0f;
+    if (t < k1) {
+        c1 = idx1[r * k1 + t];
+        v1 = val1[r * k1 + t];
+    }
     if (gate0 && !(*gate0 & kFlagError)) k0 = 0;
-    for (uint32_t j = threadIdx.x; j < k0; j += blockDim.x) {
+    for (uint32_t j = t; j < k0; j += nt) {
         const uint32_t c = idx0[r * k0 + j];
         if (c < cols) {
             if (accumulate) row[c] += val0[r * k0 + j];
@@ -660,8 +671,9 @@ __global__ void topk_scatter_kernel(const uint16_t *__restrict__ idx0, const flo
         }
     }
     if (k1 == 0) return;
-    __syncthreads();
-    for (uint32_t j = threadIdx.x; j < k1; j += blockDim.x) {
+    __syncthreads();  // the first set lands before the second (same order as the reference)
+    if (c1 < cols) row[c1] += v1;
+    for (uint32_t j = t + nt; j < k1; j += nt) {
         const uint32_t c = idx1[r * k1 + j];
         if (c < cols) row[c] += val1[r * k1 + j];
     }
@@ -732,7 +744,7 @@ void launch_topk_scatter(const uint16_t *idx0, const float *val0, uint32_t k0, c
         val1 = nullptr;
         gate0 = nullptr;
     }
-    topk_scatter_kernel<<<rows, 64, 0, stream>>>(idx0, val0, k0, idx1, val1, k1, cols, dense, accumulate, gate0);
+    topk_scatter_kernel<<<rows, 256, 0, stream>>>(idx0, val0, k0, idx1, val1, k1, cols, dense, accumulate, gate0);
     BSQ_HIP(hipGetLastError());
 }
 
