@@ -475,88 +475,222 @@ __global__ void invit_kernel(const double *__restrict__ d, const double *__restr
     for (int i = 0; i < k; ++i) z[i] = b[static_cast<uint64_t>(i) * k];
 }
 
-// LDS variants of trid_factor / trid_apply for invit_lds_kernel: the pivots
-// are stored as reciprocals so the backward pass has no division, and the
-// loops are unrolled so each step's LDS loads are issued ahead of the
-// recurrence that consumes them.
+// LDS variant of trid_factor / trid_apply for invit_lds_kernel.  Each
+// recurrence runs one eigenvalue per lane, so its operands are staged in
+// registers one chunk of kInvChunk steps ahead: the LDS round trips of a
+// chunk overlap the arithmetic of the one before (a load issued at the step
+// that needs it would put an LDS round trip on every step).  The pivots are
+// stored as reciprocals so the backward pass has no division.
+constexpr int kInvChunk = 8;
+constexpr int kInvPad = 2 * kInvChunk;  // zero entries after d and e
+
+// one elimination step of P (T - lam I) = L U; returns the new dcur.  The
+// multiplier is the quotient num / p from the hardware reciprocal with one
+// correction step (m0 + r0 (num - p m0)); the stored reciprocal of the pivot
+// takes two Newton steps.  A zero pivot is replaced by tiny.
+__device__ __forceinline__ double tridl_step(double dcur, double &ecur, double sub, double dn, double en,
+                                             double tiny, double inv_tiny, double *__restrict__ u0inv,
+                                             double *__restrict__ u1, double *__restrict__ u2,
+                                             double *__restrict__ ml, int *__restrict__ piv, int at) {
+    const bool keep = fabs(dcur) >= fabs(sub);
+    const double p = keep ? ((dcur == 0.0) ? tiny : dcur) : sub;
+    const double num = keep ? sub : dcur;
+    const double r0 = __builtin_amdgcn_rcp(p);
+    const double m0 = num * r0;
+    const double m = fma(r0, fma(-p, m0, num), m0);
+    double rp = fma(r0, fma(-p, r0, 1.0), r0);
+    rp = fma(rp, fma(-p, rp, 1.0), rp);
+    piv[at] = keep ? 0 : 1;
+    ml[at] = m;
+    u0inv[at] = (fabs(p) < tiny) ? (p < 0.0 ? -inv_tiny : inv_tiny) : rp;
+    u1[at] = keep ? ecur : dn;
+    u2[at] = keep ? 0.0 : en;
+    const double ndcur = fma(-m, keep ? ecur : dn, keep ? dn : ecur);
+    ecur = keep ? en : -m * en;
+    return ndcur;
+}
+
+// d, e: the tridiagonal in LDS, e[k - 1 ..] and d[k ..] zero (kInvPad entries)
 __device__ void tridl_factor(const double *__restrict__ d, const double *__restrict__ e, int k, double lam,
                              double tiny, double *__restrict__ u0inv, double *__restrict__ u1,
                              double *__restrict__ u2, double *__restrict__ ml, int *__restrict__ piv, int st) {
-    double dcur = d[0] - lam, ecur = (k > 1) ? e[0] : 0.0;
+    constexpr int C = kInvChunk;
     const double inv_tiny = 1.0 / tiny;
-#pragma unroll 4
-    for (int i = 0; i < k - 1; ++i) {
-        const double sub = e[i];                        // T[i+1][i]
-        const double dn = d[i + 1] - lam;               // T[i+1][i+1]
-        const double en = (i + 2 < k) ? e[i + 1] : 0.0;  // T[i+1][i+2]
-        const bool keep = fabs(dcur) >= fabs(sub);
-        const double p = keep ? ((dcur == 0.0) ? tiny : dcur) : sub;
-        // hardware reciprocal + two Newton steps instead of an IEEE division on
-        // the step-to-step chain (|p| >= |numerator|, so m is in [-1, 1])
-        double rp = __builtin_amdgcn_rcp(p);
-        rp = fma(rp, fma(-p, rp, 1.0), rp);
-        rp = fma(rp, fma(-p, rp, 1.0), rp);
-        const double m = (keep ? sub : dcur) * rp;
-        piv[i * st] = keep ? 0 : 1;
-        ml[i * st] = m;
-        // the refined reciprocal serves the backward pass too (pivots below
-        // tiny are replaced by +-tiny there, as in the division it stands for)
-        u0inv[i * st] = (fabs(p) < tiny) ? (p < 0.0 ? -inv_tiny : inv_tiny) : rp;
-        u1[i * st] = keep ? ecur : dn;
-        u2[i * st] = keep ? 0.0 : en;
-        const double ndcur = keep ? fma(-m, ecur, dn) : fma(-m, dn, ecur);
-        ecur = keep ? en : -m * en;
-        dcur = ndcur;
+    double dcur = d[0] - lam, ecur = e[0];
+    double dq[C], eq[C + 1];  // step i0 + s: d[i0 + 1 + s], e[i0 + s], e[i0 + 1 + s]
+#pragma unroll
+    for (int s = 0; s < C; ++s) dq[s] = d[1 + s];
+#pragma unroll
+    for (int s = 0; s <= C; ++s) eq[s] = e[s];
+    int i0 = 0;
+    for (; i0 + C <= k - 1; i0 += C) {
+        double dx[C], ex[C + 1];
+#pragma unroll
+        for (int s = 0; s < C; ++s) dx[s] = d[i0 + C + 1 + s];
+#pragma unroll
+        for (int s = 0; s <= C; ++s) ex[s] = e[i0 + C + s];
+#pragma unroll
+        for (int s = 0; s < C; ++s)
+            dcur = tridl_step(dcur, ecur, eq[s], dq[s] - lam, eq[s + 1], tiny, inv_tiny, u0inv, u1, u2, ml, piv,
+                              (i0 + s) * st);
+#pragma unroll
+        for (int s = 0; s < C; ++s) dq[s] = dx[s];
+#pragma unroll
+        for (int s = 0; s <= C; ++s) eq[s] = ex[s];
     }
+#pragma unroll
+    for (int s = 0; s < C; ++s)  // fewer than C steps left, operands already staged
+        if (i0 + s < k - 1)
+            dcur = tridl_step(dcur, ecur, eq[s], dq[s] - lam, eq[s + 1], tiny, inv_tiny, u0inv, u1, u2, ml, piv,
+                              (i0 + s) * st);
     u0inv[(k - 1) * st] = 1.0 / ((fabs(dcur) < tiny) ? (dcur < 0.0 ? -tiny : tiny) : dcur);
 }
 
-__device__ void tridl_apply(int k, const double *__restrict__ u0inv, const double *__restrict__ u1,
-                            const double *__restrict__ u2, const double *__restrict__ ml,
-                            const int *__restrict__ piv, int st, const double *bin, double *__restrict__ y,
-                            double *x) {
-    // forward elimination bin -> y, back substitution y -> x (x may be bin):
-    // y is a separate array, so no store of a step can alias the loads of the
-    // next ones in either pass
-    double cur = bin[0];
-#pragma unroll 8
-    for (int i = 0; i < k - 1; ++i) {
-        const double nb = bin[(i + 1) * st];
-        const bool sw = piv[i * st] != 0;
-        double nxt = sw ? cur : nb;
-        cur = sw ? nb : cur;
-        nxt = fma(-ml[i * st], cur, nxt);
-        y[i * st] = cur;
-        cur = nxt;
+// Right-hand side of a solve: the start vector of eigenvalue t (START), or
+// the previous iterate b scaled by `scale` as it is read.
+template <bool START>
+struct InvRhs {
+    const double *b;
+    double scale;
+    int t, st;
+    __device__ __forceinline__ double operator()(int i) const {
+        if constexpr (START) return start_entry(t, i);
+        else return b[i * st] * scale;
     }
-    y[(k - 1) * st] = cur;
-    double x1 = 0.0, x2 = 0.0;
-#pragma unroll 8
-    for (int i = k - 1; i >= 0; --i) {
-        double s = y[i * st];
-        s = fma(-u1[i * st], x1, s);  // u1 / u2 are 0 past the end (written by the caller)
-        s = fma(-u2[i * st], x2, s);
-        const double xi = s * u0inv[i * st];
-        x[i * st] = xi;
-        x2 = x1;
-        x1 = xi;
+};
+
+// (T - lam I) x = rhs from the factors; x (stride st) may be the array rhs
+// reads.  u1 / u2 must be zero in row k - 1 and u2 in row k - 2.  Returns
+// sum x_i^2.
+template <class Rhs>
+__device__ double tridl_solve(int k, const double *__restrict__ u0inv, const double *__restrict__ u1,
+                              const double *__restrict__ u2, const double *__restrict__ ml,
+                              const int *__restrict__ piv, int st, const Rhs &rhs, double *__restrict__ y,
+                              double *x) {
+    constexpr int C = kInvChunk;
+    // forward elimination rhs -> y (step i: rhs(i + 1), piv[i], ml[i])
+    double cur = rhs(0);
+    {
+        double nb[C], mq[C];
+        int pq[C];
+        const int full = (k - 1) / C * C;
+        if (full > 0) {
+#pragma unroll
+            for (int s = 0; s < C; ++s) {
+                nb[s] = rhs(1 + s);
+                mq[s] = ml[s * st];
+                pq[s] = piv[s * st];
+            }
+        }
+        for (int i0 = 0; i0 < full; i0 += C) {
+            double nbx[C], mx[C];
+            int px[C];
+            if (i0 + C < full) {
+#pragma unroll
+                for (int s = 0; s < C; ++s) {
+                    nbx[s] = rhs(i0 + C + 1 + s);
+                    mx[s] = ml[(i0 + C + s) * st];
+                    px[s] = piv[(i0 + C + s) * st];
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < C; ++s) {
+                const bool sw = pq[s] != 0;
+                double nxt = sw ? cur : nb[s];
+                cur = sw ? nb[s] : cur;
+                nxt = fma(-mq[s], cur, nxt);
+                y[(i0 + s) * st] = cur;
+                cur = nxt;
+            }
+#pragma unroll
+            for (int s = 0; s < C; ++s) {
+                nb[s] = nbx[s];
+                mq[s] = mx[s];
+                pq[s] = px[s];
+            }
+        }
+        for (int i = full; i < k - 1; ++i) {
+            const double v = rhs(i + 1);
+            const bool sw = piv[i * st] != 0;
+            double nxt = sw ? cur : v;
+            cur = sw ? v : cur;
+            nxt = fma(-ml[i * st], cur, nxt);
+            y[i * st] = cur;
+            cur = nxt;
+        }
+        y[(k - 1) * st] = cur;
     }
+    // back substitution y -> x; the term of the older unknown is added first
+    double x1 = 0.0, x2 = 0.0, n0 = 0.0, n1 = 0.0;
+    {
+        double yq[C], aq[C], bq[C], rq[C];  // step i = top - s
+        const int rem = k % C;  // the top rem rows first, then full chunks
+        int top = k - 1;
+        for (; top >= k - rem; --top) {
+            const double s1 = fma(-u2[top * st], x2, y[top * st]);
+            const double xi = fma(-u1[top * st], x1, s1) * u0inv[top * st];
+            x[top * st] = xi;
+            n0 = fma(xi, xi, n0);
+            x2 = x1;
+            x1 = xi;
+        }
+        if (top >= 0) {
+#pragma unroll
+            for (int s = 0; s < C; ++s) {
+                const int i = top - s;
+                yq[s] = y[i * st];
+                aq[s] = u1[i * st];
+                bq[s] = u2[i * st];
+                rq[s] = u0inv[i * st];
+            }
+        }
+        for (; top >= 0; top -= C) {
+            double yx[C], ax[C], bx[C], rx[C];
+            if (top - C >= 0) {
+#pragma unroll
+                for (int s = 0; s < C; ++s) {
+                    const int i = top - C - s;
+                    yx[s] = y[i * st];
+                    ax[s] = u1[i * st];
+                    bx[s] = u2[i * st];
+                    rx[s] = u0inv[i * st];
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < C; ++s) {
+                const double s1 = fma(-bq[s], x2, yq[s]);
+                const double xi = fma(-aq[s], x1, s1) * rq[s];
+                x[(top - s) * st] = xi;
+                if (s & 1) n1 = fma(xi, xi, n1);
+                else n0 = fma(xi, xi, n0);
+                x2 = x1;
+                x1 = xi;
+            }
+#pragma unroll
+            for (int s = 0; s < C; ++s) {
+                yq[s] = yx[s];
+                aq[s] = ax[s];
+                bq[s] = bx[s];
+                rq[s] = rx[s];
+            }
+        }
+    }
+    return n0 + n1;
 }
 
 // The same inverse iteration with every per-eigenvalue array in LDS: lane j
 // (< P) of a one-wave workgroup handles eigenvalue blockIdx.x * P + j, its
-// element i at i * P + j.  The recurrences are sequential per eigenvalue, so
-// what bounds them is the latency of each step's loads: LDS instead of L2.
+// element i at i * P + j.
 __global__ __launch_bounds__(64) void invit_lds_kernel(const double *__restrict__ d, const double *__restrict__ e,
                                                        int k, int P, const double *__restrict__ lambda,
                                                        const double *__restrict__ tnorm_p, double *__restrict__ Z) {
     extern __shared__ double sm[];
     const uint64_t kp = static_cast<uint64_t>(k) * P;
     double *u0 = sm, *u1 = u0 + kp, *u2 = u1 + kp, *ml = u2 + kp, *b = ml + kp, *yv = b + kp, *ds = yv + kp,
-           *es = ds + k;
-    int *piv = reinterpret_cast<int *>(es + k);
-    for (int i = threadIdx.x; i < k; i += blockDim.x) {
-        ds[i] = d[i];
+           *es = ds + k + kInvPad;
+    int *piv = reinterpret_cast<int *>(es + k + kInvPad);
+    for (int i = threadIdx.x; i < k + kInvPad; i += blockDim.x) {
+        ds[i] = (i < k) ? d[i] : 0.0;
         es[i] = (i + 1 < k) ? e[i] : 0.0;
     }
     __syncthreads();
@@ -564,32 +698,24 @@ __global__ __launch_bounds__(64) void invit_lds_kernel(const double *__restrict_
     if (j >= P || t >= k) return;  // no barrier below
     const double tnorm = fmax(tnorm_p[0], DBL_MIN);
     const double tiny = tnorm * DBL_EPSILON;
-    // the last row of u1 / u2 is read by the backward pass of the last step
+    // rows the factorisation leaves unwritten but the back substitution reads
+    // (times a zero unknown)
     u1[(k - 1) * P + j] = 0.0;
     u2[(k - 1) * P + j] = 0.0;
     if (k >= 2) u2[(k - 2) * P + j] = 0.0;
     tridl_factor(ds, es, k, lambda[t], tiny, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P);
-    for (int i = 0; i < k; ++i) b[i * P + j] = start_entry(t, i);
     // two solves: lambda is within k * eps * ||T|| of the eigenvalue, so one
     // solve already grows the wanted component by ~1 / (k eps) over components
     // separated by more than the clustering tolerance (closer ones are redone
-    // by cluster_kernel); the second leaves the iterate at working accuracy
-    for (int it = 0; it < 2; ++it) {
-        tridl_apply(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, b + j, yv + j, b + j);
-        double n0 = 0.0, n1 = 0.0;
-#pragma unroll 4
-        for (int i = 0; i < k; i += 2) {
-            const double b0 = b[i * P + j], b1 = (i + 1 < k) ? b[(i + 1) * P + j] : 0.0;
-            n0 = fma(b0, b0, n0);
-            n1 = fma(b1, b1, n1);
-        }
-        const double nrm = n0 + n1;
-        const double inv = nrm > 0.0 ? 1.0 / sqrt(nrm) : 0.0;
-#pragma unroll 4
-        for (int i = 0; i < k; ++i) b[i * P + j] *= inv;
-    }
+    // by cluster_kernel); the second leaves the iterate at working accuracy.
+    // The first iterate's normalisation is applied as the second solve reads it.
+    const InvRhs<true> start{nullptr, 1.0, t, P};
+    const double n1 = tridl_solve(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, start, yv + j, b + j);
+    const InvRhs<false> again{b + j, n1 > 0.0 ? 1.0 / sqrt(n1) : 0.0, t, P};
+    const double n2 = tridl_solve(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, again, yv + j, b + j);
+    const double inv = n2 > 0.0 ? 1.0 / sqrt(n2) : 0.0;
     double *z = Z + static_cast<uint64_t>(t) * k;
-    for (int i = 0; i < k; ++i) z[i] = b[i * P + j];
+    for (int i = 0; i < k; ++i) z[i] = b[i * P + j] * inv;
 }
 
 // Re-runs inverse iteration for eigenvalue clusters (gap below
@@ -887,11 +1013,13 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
     BSQ_HIP(hipGetLastError());
     multisect_kernel<<<k, kMsThreads, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);
     BSQ_HIP(hipGetLastError());
-    // eigenvalues per workgroup whose LDS arrays fit: (6kP + 2k) doubles + kP ints
+    // eigenvalues per workgroup whose LDS arrays fit: (6kP + 2(k + pad)) doubles + kP ints
     const int64_t lds_cap = 160 * 1024;
-    const int P = static_cast<int>(std::min<int64_t>(8, (lds_cap - 16 * static_cast<int64_t>(k)) / (52 * static_cast<int64_t>(k))));
+    const int64_t pad_bytes = 16 * (static_cast<int64_t>(k) + kInvPad);
+    const int P = static_cast<int>(std::min<int64_t>(8, (lds_cap - pad_bytes) / (52 * static_cast<int64_t>(k))));
     if (P >= 1) {
-        const size_t lds = (6 * static_cast<size_t>(k) * P + 2 * k) * sizeof(double) + static_cast<size_t>(k) * P * sizeof(int);
+        const size_t lds = (6 * static_cast<size_t>(k) * P + 2 * (k + kInvPad)) * sizeof(double) +
+                           static_cast<size_t>(k) * P * sizeof(int);
         BSQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(invit_lds_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         invit_lds_kernel<<<static_cast<unsigned>(ceil_div(k, P)), 64, lds, stream>>>(d, e, k, P, lambda, tn, Z);
