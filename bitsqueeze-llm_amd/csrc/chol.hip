@@ -13,9 +13,9 @@
 //                         the workgroup synchronises ~50 times instead of
 //                         ~1500.  Breakdown (pivot <= 1e-15 max|G_ii|) restarts
 //                         with a diagonal shift, as the unblocked version does.
-//   trinv_kernel          L^{-1} by blocked forward substitution, 8 columns
-//                         per workgroup, so the inverse is spread over
-//                         k / 8 CUs instead of one.  Writes B = L^{-T} in
+//   trinv_kernel          L^{-1} by blocked forward substitution on the FP64
+//                         matrix cores, 16 columns per workgroup, so the
+//                         inverse is spread over k / 16 CUs.  Writes B = L^{-T} in
 //                         FP32 row-major (B[r][c] = L^{-1}[c][r]) so that the
 //                         orthonormal basis is the plain product Q = X B.
 //
@@ -275,40 +275,128 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
     if (tid == 0 && status) status[0] = attempt;
 }
 
-// Columns c0 .. c0+7 of L^{-1}, block row by block row:
-//   X_cb = LI_cb[:, cols];  X_i = -LI_i * sum_{t=cb}^{i-1} L_it X_t
+// Columns c0 .. c0+15 of L^{-1}, block row by block row, on the FP64 matrix
+// cores (v_mfma_f64_16x16x4f64):
+//   X_cb = LI_cb[:, cols];  X_i = -LI_i * S_i,  S_i = sum_{t=cb}^{i-1} L_it X_t
+// L and LI were written by a kernel on another XCD, so every piece of them
+// this workgroup needs is loaded at the start, all in flight at once (1024
+// lanes hold the widest strip in ~80 registers each: one memory latency
+// instead of one per block row).  Block row i's panel L[i rows][cb * 32 ..
+// i * 32) and LI_i then go from registers to LDS, and S_i (32 x 16, K =
+// 32 (i - cb)) is formed by 16 waves (rh, kh): rows rh * 16 .. +16 over the
+// k-steps s = kh (mod 8), the eight partial sums added through LDS; waves 0
+// and 1 apply the lower-triangular LI_i.
+// MFMA operand lanes: A[r][q] and B[q][c] in lane 16 q + (r or c);
+// accumulator register u of lane l holds D[4 u + l / 16][l % 16].
 // Output B = L^{-T} (k x k FP32 row-major): B[c][r] = L^{-1}[r][c].
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+constexpr int kTrinvThreads = 1024;
+
 template <int NB>
-__global__ __launch_bounds__(256) void trinv_kernel(const double *__restrict__ Lin, const double *__restrict__ LIin,
-                                                    int k, float *__restrict__ B, const int *__restrict__ run) {
+__global__ __launch_bounds__(kTrinvThreads) void trinv_kernel(const double *__restrict__ Lin,
+                                                              const double *__restrict__ LIin, int k,
+                                                              float *__restrict__ B, const int *__restrict__ run) {
     if (run && run[0] == 0) return;  // uniform
     constexpr int KP = NB * 32;
-    __shared__ double X[KP][8];
-    __shared__ double S[32][8];
-    const int c0 = blockIdx.x * 8, cb = c0 >> 5, co = c0 & 31;
-    const int tid = threadIdx.x, rr = tid >> 3, j = tid & 7;
-    X[cb * 32 + rr][j] = LIin[static_cast<uint64_t>(cb) * 1024 + rr * 32 + co + j];
-    __syncthreads();
-    for (int i = cb + 1; i < NB; ++i) {
-        const double *lrow = Lin + static_cast<uint64_t>(i * 32 + rr) * KP;
-        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-        for (int col = cb * 32; col < i * 32; col += 4) {
-            s0 = fma(lrow[col + 0], X[col + 0][j], s0);
-            s1 = fma(lrow[col + 1], X[col + 1][j], s1);
-            s2 = fma(lrow[col + 2], X[col + 2][j], s2);
-            s3 = fma(lrow[col + 3], X[col + 3][j], s3);
+    constexpr int PP = (NB > 1 ? 32 * (NB - 1) : 32) + 4;  // panel pitch (doubles): 2-way banks for the A reads
+    constexpr int XP = 17, LP = 36;
+    // panel d (1 .. NB - 1): row lr, 16-byte pieces lp + 32 u, u < (d + 1) / 2
+    constexpr int kPanelPieces = (NB * NB) / 4 + 1;  // >= sum_d (d + 1) / 2 for d < NB
+    constexpr int kLiPieces = (NB > 1) ? ((NB - 1) * 512 + kTrinvThreads - 1) / kTrinvThreads : 1;
+    __shared__ __attribute__((aligned(16))) double P[32][PP];
+    __shared__ __attribute__((aligned(16))) double LIs[32][LP];
+    __shared__ double X[KP][XP];
+    __shared__ double SP[8][32][XP];
+    __shared__ double S[32][XP];
+    const int c0 = blockIdx.x * 16, cb = c0 >> 5, co = c0 & 31;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kq = lane >> 4, cc = lane & 15;
+    const int rh = wave & 1, kh = wave >> 1;
+    const int lr = tid >> 5, lp = tid & 31;
+    const int nsteps = NB - 1 - cb;
+
+    double pv[2 * kPanelPieces], lv[2 * kLiPieces];
+    if (nsteps >= 1) {  // uniform (the last column block has no panels)
+        int at = 0;
+#pragma unroll
+        for (int d = 1; d < NB; ++d) {
+            const int dd = d <= nsteps ? d : 1;  // panels past the strip re-read panel 1 (not stored)
+            const double2 *prow =
+                reinterpret_cast<const double2 *>(Lin + static_cast<uint64_t>((cb + dd) * 32 + lr) * KP + cb * 32);
+#pragma unroll
+            for (int u = 0; u < (d + 1) / 2; ++u) {
+                const double2 v = prow[min(lp + 32 * u, 16 * dd - 1)];
+                pv[2 * at] = v.x;
+                pv[2 * at + 1] = v.y;
+                ++at;
+            }
         }
-        S[rr][j] = (s0 + s1) + (s2 + s3);
-        __syncthreads();
-        const double *li = LIin + static_cast<uint64_t>(i) * 1024 + rr * 32;
-        double x = 0.0;
-        for (int u = 0; u <= rr; ++u) x = fma(li[u], S[u][j], x);
-        X[i * 32 + rr][j] = -x;
-        __syncthreads();
+#pragma unroll
+        for (int v = 0; v < kLiPieces; ++v) {
+            const int q = min(tid + kTrinvThreads * v, 512 * nsteps - 1);  // piece of blocks cb+1 ..
+            const double2 w = reinterpret_cast<const double2 *>(LIin + static_cast<uint64_t>(cb + 1) * 1024)[q];
+            lv[2 * v] = w.x;
+            lv[2 * v + 1] = w.y;
+        }
     }
-    for (int t = tid; t < 8 * k; t += 256) {
-        const int jj = t / k, r = t % k, c = c0 + jj;
-        if (c < k) B[static_cast<uint64_t>(c) * k + r] = (r >= cb * 32) ? static_cast<float>(X[r][jj]) : 0.0f;
+    for (int t = tid; t < 32 * 16; t += kTrinvThreads) {
+        const int r = t >> 4, j = t & 15;
+        X[cb * 32 + r][j] = LIin[static_cast<uint64_t>(cb) * 1024 + r * 32 + co + j];
+    }
+    int at0 = 0;  // first panel piece of step d
+#pragma unroll
+    for (int d = 1; d < NB; ++d) {
+        if (d <= nsteps) {  // uniform
+            // panel d and LI_{cb+d} into LDS (the previous step's readers are done)
+#pragma unroll
+            for (int u = 0; u < (d + 1) / 2; ++u)
+                if (lp + 32 * u < 16 * d)
+                    *reinterpret_cast<double2 *>(&P[lr][2 * (lp + 32 * u)]) =
+                        double2{pv[2 * (at0 + u)], pv[2 * (at0 + u) + 1]};
+#pragma unroll
+            for (int v = 0; v < kLiPieces; ++v) {
+                const int q = tid + kTrinvThreads * v;
+                if ((q >> 9) == d - 1) *reinterpret_cast<double2 *>(&LIs[(q >> 4) & 31][2 * (q & 15)]) =
+                    double2{lv[2 * v], lv[2 * v + 1]};
+            }
+            __syncthreads();
+            // S partials: wave (rh, kh) over k-steps s = kh + 8 j, j < d
+            f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int j = 0; j < d; ++j) {
+                const int s = kh + 8 * j;
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(P[rh * 16 + cc][4 * s + kq], X[cb * 32 + 4 * s + kq][cc],
+                                                           acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) SP[kh][rh * 16 + 4 * u + kq][cc] = acc[u];
+            __syncthreads();
+            if (tid < 512) {
+                const int r = tid >> 4, c = tid & 15;
+                double t = SP[0][r][c];
+#pragma unroll
+                for (int h = 1; h < 8; ++h) t += SP[h][r][c];
+                S[r][c] = t;
+            }
+            __syncthreads();
+            if (wave < 2) {  // wave-uniform; LI_i lower triangular: rows 0..15 need only k < 16
+                f64x4 t = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+                    if (rh == 1 || s < 4)
+                        t = __builtin_amdgcn_mfma_f64_16x16x4f64(LIs[rh * 16 + cc][4 * s + kq], S[4 * s + kq][cc], t,
+                                                                 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) X[(cb + d) * 32 + rh * 16 + 4 * u + kq][cc] = -t[u];
+            }
+            __syncthreads();
+        }
+        at0 += (d + 1) / 2;
+    }
+    for (int jj = 0; jj < 16 && c0 + jj < k; ++jj) {
+        float *brow = B + static_cast<uint64_t>(c0 + jj) * k;
+        for (int r = tid; r < k; r += kTrinvThreads)
+            brow[r] = (r >= cb * 32) ? static_cast<float>(X[r][jj]) : 0.0f;
     }
 }
 
@@ -317,7 +405,7 @@ void chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, c
     double *L = Lbuf, *LI = Lbuf + static_cast<uint64_t>(NB) * 32 * NB * 32;
     chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, status, run);
     BSQ_HIP(hipGetLastError());
-    trinv_kernel<NB><<<static_cast<unsigned>(ceil_div(k, 8)), 256, 0, stream>>>(L, LI, k, B, run);
+    trinv_kernel<NB><<<static_cast<unsigned>(ceil_div(k, 16)), kTrinvThreads, 0, stream>>>(L, LI, k, B, run);
     BSQ_HIP(hipGetLastError());
 }
 
