@@ -361,9 +361,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 constexpr int kStages = 4;
-constexpr int kTileF = 128 * BK;              // floats per operand tile (8 KB)
-constexpr int kStageF = 2 * kTileF;           // A + B
-constexpr int kDmaReconMaxK = 1024;           // RECON column scales staged in LDS
+constexpr int kDmaReconMaxK = 1024;  // RECON column scales staged in LDS
 
 __device__ __forceinline__ void dma16(const float *g, const float *l) {
     __builtin_amdgcn_global_load_lds((glb_void_t *)(g), (lds_void_t *)(reinterpret_cast<size_t>(l)), 16, 0, 0);
@@ -379,8 +377,18 @@ __device__ __forceinline__ void dma_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// one 1 KB chunk c (0..7) of a 128 x 16 tile
-template <bool KMAJOR>
+// one 1 KB chunk c (0 .. T/16 - 1) of a T x 16 operand tile (T = 128 or 64)
+//   k-contiguous operand [row][k]: 16 rows per chunk, 16-byte quads of a row
+//     XOR-swizzled by bits 1..2 of the row;
+//   k-major operand [k][col]: 1024 / (4 T) k-rows per chunk, quads of a k-row
+//     XOR-swizzled so that the four k-rows one fragment read touches fall in
+//     different banks.
+template <bool KMAJOR, int T>
+__device__ __forceinline__ int kmajor_swizzle(int kr) {  // column XOR of k-row kr
+    if constexpr (T == 128) return 16 * ((kr >> 2) & 1);
+    else return 16 * ((kr >> 2) & 3);
+}
+template <bool KMAJOR, int T>
 __device__ __forceinline__ void dma_chunk(const float *__restrict__ P, int ld, int r0, int extent, int k0, int c,
                                           const float *lds_tile) {
     const int l = threadIdx.x & 63;
@@ -390,14 +398,15 @@ __device__ __forceinline__ void dma_chunk(const float *__restrict__ P, int ld, i
         const int gr = min(r0 + r, extent - 1);
         dma16(P + static_cast<uint64_t>(gr) * ld + k0 + 4 * q, lds_tile + c * 256);
     } else {  // P row-major [k][col]
-        const int kr = 2 * c + (l >> 5);
-        const int cq = (l & 31) ^ (4 * ((kr >> 2) & 1));
+        constexpr int QPR = T / 4;  // quads per k-row
+        const int kr = (64 / QPR) * c + l / QPR;
+        const int cq = (l % QPR) ^ (kmajor_swizzle<KMAJOR, T>(kr) / 4);
         const int gc = min(r0 + 4 * cq, extent - 4);
         dma16(P + static_cast<uint64_t>(k0 + kr) * ld + gc, lds_tile + c * 256);
     }
 }
 
-template <bool KMAJOR>
+template <bool KMAJOR, int T>
 __device__ __forceinline__ void dma_frag(const float *S, int row, int kk, float (&o)[KS]) {
     if constexpr (!KMAJOR) {
         const float4 v = *reinterpret_cast<const float4 *>(&S[row * 16 + 4 * (kk ^ ((row >> 1) & 3))]);
@@ -406,14 +415,25 @@ __device__ __forceinline__ void dma_frag(const float *S, int row, int kk, float 
         o[2] = v.z;
         o[3] = v.w;
     } else {
-        const int sw = 16 * (kk & 1);
 #pragma unroll
-        for (int s = 0; s < KS; ++s) o[s] = S[(4 * kk + s) * 128 + (row ^ sw)];
+        for (int s = 0; s < KS; ++s) {
+            const int kr = 4 * kk + s;
+            o[s] = S[kr * T + (row ^ kmajor_swizzle<KMAJOR, T>(kr))];
+        }
     }
 }
 
-template <bool TA, bool TB, bool RECON>
+// T x T output tile (T = 128, or 64 for grids that 128-wide tiles would
+// leave short of the CU count); four waves of T/2 x T/2.
+template <bool TA, bool TB, bool RECON, int T>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
+    static_assert(T == 128 || (T == 64 && !RECON), "gemm: tile size");
+    constexpr int BM = T, BN = T;
+    constexpr int kTileF = T * BK;     // floats per operand tile
+    constexpr int kStageF = 2 * kTileF;  // A + B
+    constexpr int kChunks = T / 16;    // 1 KB DMA chunks per operand tile
+    constexpr int kCpw = kChunks / 4;  // chunks per wave per operand
+    constexpr int kDmaPerSlice = 2 * kCpw;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 16, FN = WN / 16;
     // one LDS object per stage: the compiler's wait insertion then sees that a
@@ -443,14 +463,14 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
         for (int t = tid; t < kend - kbeg; t += kThreads) scs[t] = g.a_colscale ? g.a_colscale[kbeg + t] : 1.0f;
         // visible after the first barrier of the loop
     }
-    // each wave issues chunks 2w, 2w+1 of A and of B: four DMAs per slice
+    // each wave issues chunks kCpw w .. kCpw w + kCpw - 1 of A and of B
     auto issue = [&](const float *st, int j) {
         const int k0 = kbeg + j * BK;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int c = 2 * wave + h;
-            dma_chunk<TA>(g.A, g.lda, m0, g.M, k0, c, st);
-            dma_chunk<!TB>(g.B, g.ldb, n0, g.N, k0, c, st + kTileF);
+        for (int h = 0; h < kCpw; ++h) {
+            const int c = kCpw * wave + h;
+            dma_chunk<TA, T>(g.A, g.lda, m0, g.M, k0, c, st);
+            dma_chunk<!TB, T>(g.B, g.ldb, n0, g.N, k0, c, st + kTileF);
         }
     };
     const int kk = lane >> 4, cc = lane & 15;
@@ -458,13 +478,13 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
     // in iteration j - 1) receives slice j + 3
     auto body = [&](const float *cur, const float *nxt, int j) {
         const int ahead = min(kStages - 2, nk - 1 - j);  // slices issued after j
-        if (ahead >= 2) dma_barrier<8>();
-        else if (ahead == 1) dma_barrier<4>();
+        if (ahead >= 2) dma_barrier<2 * kDmaPerSlice>();
+        else if (ahead == 1) dma_barrier<kDmaPerSlice>();
         else dma_barrier<0>();
         if (j + kStages - 1 < nk) issue(nxt, j + kStages - 1);
         float a[FM][KS], b[FN][KS];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) dma_frag<TA>(cur, wm0 + i * 16 + cc, kk, a[i]);
+        for (int i = 0; i < FM; ++i) dma_frag<TA, T>(cur, wm0 + i * 16 + cc, kk, a[i]);
         if constexpr (RECON) {
 #pragma unroll
             for (int s2 = 0; s2 < KS; ++s2) {
@@ -474,7 +494,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
             }
         }
 #pragma unroll
-        for (int jj = 0; jj < FN; ++jj) dma_frag<!TB>(cur + kTileF, wn0 + jj * 16 + cc, kk, b[jj]);
+        for (int jj = 0; jj < FN; ++jj) dma_frag<!TB, T>(cur + kTileF, wn0 + jj * 16 + cc, kk, b[jj]);
 #pragma unroll
         for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
@@ -656,14 +676,24 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
     // register-staged one
     const bool dma = g.vec_a && g.vec_b && (K % BK == 0) && (!ta || M % 4 == 0) &&
                      (tb || N % 4 == 0) && (!recon || K <= kDmaReconMaxK);
-    if (dma) {
+    // 64 x 64 tiles when 128 x 128 ones (unsplit) would not give every CU two
+    // workgroups: the short-K products of the orthonormalisation
+    const bool t64 = dma && !recon && splits == 1 &&
+                     ceil_div(M, BM) * ceil_div(N, BN) < 2 * static_cast<uint64_t>(cu_count());
+    if (t64) {
+        grid.x = static_cast<unsigned>(ceil_div(N, 64) * ceil_div(M, 64));
+        if (!ta && !tb) gemm_dma_kernel<false, false, false, 64><<<grid, kThreads, 0, stream>>>(g);
+        else if (ta && !tb) gemm_dma_kernel<true, false, false, 64><<<grid, kThreads, 0, stream>>>(g);
+        else if (!ta && tb) gemm_dma_kernel<false, true, false, 64><<<grid, kThreads, 0, stream>>>(g);
+        else gemm_dma_kernel<true, true, false, 64><<<grid, kThreads, 0, stream>>>(g);
+    } else if (dma) {
         if (recon) {
             BSQ_REQUIRE(!ta && tb, "gemm: column scale / minuend only in the A * B^T form");
-            gemm_dma_kernel<false, true, true><<<grid, kThreads, 0, stream>>>(g);
-        } else if (!ta && !tb) gemm_dma_kernel<false, false, false><<<grid, kThreads, 0, stream>>>(g);
-        else if (ta && !tb) gemm_dma_kernel<true, false, false><<<grid, kThreads, 0, stream>>>(g);
-        else if (!ta && tb) gemm_dma_kernel<false, true, false><<<grid, kThreads, 0, stream>>>(g);
-        else gemm_dma_kernel<true, true, false><<<grid, kThreads, 0, stream>>>(g);
+            gemm_dma_kernel<false, true, true, 128><<<grid, kThreads, 0, stream>>>(g);
+        } else if (!ta && !tb) gemm_dma_kernel<false, false, false, 128><<<grid, kThreads, 0, stream>>>(g);
+        else if (ta && !tb) gemm_dma_kernel<true, false, false, 128><<<grid, kThreads, 0, stream>>>(g);
+        else if (!ta && tb) gemm_dma_kernel<false, true, false, 128><<<grid, kThreads, 0, stream>>>(g);
+        else gemm_dma_kernel<true, true, false, 128><<<grid, kThreads, 0, stream>>>(g);
     } else if (recon) {
         BSQ_REQUIRE(!ta && tb, "gemm: column scale / minuend only in the A * B^T form");
         gemm_mfma_kernel<false, true, true><<<grid, kThreads, 0, stream>>>(g);

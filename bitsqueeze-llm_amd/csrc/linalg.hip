@@ -49,40 +49,45 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
     const int r0 = blockIdx.y * rows_per_split, r1 = min(M, r0 + rows_per_split);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wi = (wave >> 1) * 32, wj = (wave & 1) * 32;
-    // staging: 32 rows x 64 columns = 512 float4, two per lane per operand
-    float4 pi[2], pj[2];
-    auto fetch = [&](int rb) {
+    // staging: 32 rows x 64 columns = 512 float4, two per lane per operand.
+    // A chunk's loads are issued three chunks ahead of its multiply (a ring
+    // of four register sets): one chunk's MFMAs take a fraction of a memory
+    // latency, so a single chunk of lookahead would leave the MFMAs waiting.
+    struct Stage {
+        float4 i[2], j[2];
+    };
+    auto fetch = [&](int rb, Stage &st) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int lin = tid + 256 * q, rr = lin >> 4, c4 = (lin & 15) * 4;
             const int r = rb + rr, ci = ti * kGramTile + c4, cj = tj * kGramTile + c4;
             const float *row = X + static_cast<uint64_t>(r) * ld;
             if (vec && r < r1 && ci + 4 <= k) {
-                pi[q] = *reinterpret_cast<const float4 *>(row + ci);
+                st.i[q] = *reinterpret_cast<const float4 *>(row + ci);
             } else {
-                pi[q].x = (r < r1 && ci + 0 < k) ? row[ci + 0] : 0.0f;
-                pi[q].y = (r < r1 && ci + 1 < k) ? row[ci + 1] : 0.0f;
-                pi[q].z = (r < r1 && ci + 2 < k) ? row[ci + 2] : 0.0f;
-                pi[q].w = (r < r1 && ci + 3 < k) ? row[ci + 3] : 0.0f;
+                st.i[q].x = (r < r1 && ci + 0 < k) ? row[ci + 0] : 0.0f;
+                st.i[q].y = (r < r1 && ci + 1 < k) ? row[ci + 1] : 0.0f;
+                st.i[q].z = (r < r1 && ci + 2 < k) ? row[ci + 2] : 0.0f;
+                st.i[q].w = (r < r1 && ci + 3 < k) ? row[ci + 3] : 0.0f;
             }
             if (!diag) {
                 if (vec && r < r1 && cj + 4 <= k) {
-                    pj[q] = *reinterpret_cast<const float4 *>(row + cj);
+                    st.j[q] = *reinterpret_cast<const float4 *>(row + cj);
                 } else {
-                    pj[q].x = (r < r1 && cj + 0 < k) ? row[cj + 0] : 0.0f;
-                    pj[q].y = (r < r1 && cj + 1 < k) ? row[cj + 1] : 0.0f;
-                    pj[q].z = (r < r1 && cj + 2 < k) ? row[cj + 2] : 0.0f;
-                    pj[q].w = (r < r1 && cj + 3 < k) ? row[cj + 3] : 0.0f;
+                    st.j[q].x = (r < r1 && cj + 0 < k) ? row[cj + 0] : 0.0f;
+                    st.j[q].y = (r < r1 && cj + 1 < k) ? row[cj + 1] : 0.0f;
+                    st.j[q].z = (r < r1 && cj + 2 < k) ? row[cj + 2] : 0.0f;
+                    st.j[q].w = (r < r1 && cj + 3 < k) ? row[cj + 3] : 0.0f;
                 }
             }
         }
     };
-    auto put = [&](int b) {
+    auto put = [&](int b, const Stage &st) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int lin = tid + 256 * q, rr = lin >> 4, c4 = (lin & 15) * 4;
-            *reinterpret_cast<float4 *>(&xi[b][rr][c4]) = pi[q];
-            if (!diag) *reinterpret_cast<float4 *>(&xj[b][rr][c4]) = pj[q];
+            *reinterpret_cast<float4 *>(&xi[b][rr][c4]) = st.i[q];
+            if (!diag) *reinterpret_cast<float4 *>(&xj[b][rr][c4]) = st.j[q];
         }
     };
     f64x4 acc[2][2];
@@ -90,18 +95,10 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
     for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) acc[a][b] = f64x4{0.0, 0.0, 0.0, 0.0};
-    int buf = 0;
-    if (r0 < r1) {
-        fetch(r0);
-        put(0);
-    }
-    __syncthreads();
     const int kk = lane >> 4, cc = lane & 15;
-    for (int rb = r0; rb < r1; rb += kGramRows) {
-        const bool more = rb + kGramRows < r1;
-        if (more) fetch(rb + kGramRows);
-        const float(*BI)[kGramPitch] = xi[buf];
-        const float(*BJ)[kGramPitch] = diag ? xi[buf] : xj[buf];
+    auto multiply = [&](int b) {
+        const float(*BI)[kGramPitch] = xi[b];
+        const float(*BJ)[kGramPitch] = diag ? xi[b] : xj[b];
 #pragma unroll
         for (int st = 0; st < kGramRows / 4; ++st) {
             const int rr = 4 * st + kk;
@@ -109,15 +106,33 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
 #pragma unroll
             for (int a = 0; a < 2; ++a) av[a] = static_cast<double>(BI[rr][wi + 16 * a + cc]);
 #pragma unroll
-            for (int b = 0; b < 2; ++b) bv[b] = static_cast<double>(BJ[rr][wj + 16 * b + cc]);
+            for (int b2 = 0; b2 < 2; ++b2) bv[b2] = static_cast<double>(BJ[rr][wj + 16 * b2 + cc]);
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
-                for (int b = 0; b < 2; ++b) acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
+                for (int b2 = 0; b2 < 2; ++b2)
+                    acc[a][b2] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b2], acc[a][b2], 0, 0, 0);
         }
-        if (more) put(buf ^ 1);
+    };
+    const int nch = r0 < r1 ? static_cast<int>(ceil_div(r1 - r0, kGramRows)) : 0;
+    Stage s0, s1, s2, s3;
+    if (nch > 0) fetch(r0, s0);
+    if (nch > 1) fetch(r0 + kGramRows, s1);
+    if (nch > 2) fetch(r0 + 2 * kGramRows, s2);
+    if (nch > 0) put(0, s0);
+    __syncthreads();
+    // chunk c sits in register set c % 4 until it is put into LDS buffer c % 2
+    auto step = [&](int c, Stage &ahead, const Stage &next) {
+        if (c + 3 < nch) fetch(r0 + (c + 3) * kGramRows, ahead);
+        multiply(c & 1);
+        if (c + 1 < nch) put((c + 1) & 1, next);
         __syncthreads();
-        buf ^= 1;
+    };
+    for (int c = 0; c < nch; c += 4) {
+        step(c, s3, s1);
+        if (c + 1 < nch) step(c + 1, s0, s2);
+        if (c + 2 < nch) step(c + 2, s1, s3);
+        if (c + 3 < nch) step(c + 3, s2, s0);
     }
     double *out = P + static_cast<uint64_t>(blockIdx.y) * k * k;
 #pragma unroll
