@@ -11,7 +11,7 @@ this host.
 
 Dominant kernel: on the SVD workloads, the FP32-MFMA GEMM that touches the
 full matrix; the one timed is the low-rank reconstruction
-U diag(S) V^T (gemm_dma_kernel<false, true, true>), bracketed with HIP
+U diag(S) V^T (gemm_dma_kernel<false, true, true, 128>), bracketed with HIP
 events on the runtime stream inside the timed steps (2 * rows * cols * rank
 flops per launch, twice per step).  On the direct workloads, the NF4 / NF4_DQ
 encode of the full matrix (read 4N bytes, write the section), timed with HIP
@@ -282,7 +282,7 @@ def main():
         roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
                     "traffic": committed_traffic(tag, args.workload),
-                    "kernel": "gemm_dma_kernel<false, true, true> (U diag(S) V^T, FP32 MFMA)",
+                    "kernel": "gemm_dma_kernel<false, true, true, 128> (U diag(S) V^T, FP32 MFMA)",
                     "avg_ms": round(kms, 5), "launches": launches, "alg_flops": kflops}
     else:
         kname, kms, kbytes = time_dominant_kernel(wl, rows, cols, dsrc, stream)

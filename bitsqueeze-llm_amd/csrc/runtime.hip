@@ -986,6 +986,24 @@ uint64_t bitsqz_llm_get_packed_size(const bitsqz_llm_array_t *c) {
     return static_cast<uint64_t>(sizeof(bitsqz_llm_array_t)) + payload;
 }
 
+// The payload end of the six sections without wrapping: false when 200 plus
+// the largest end does not fit in 64 bits.  The reference sums in wrapping
+// u64 arithmetic (src/bitsqz_llm.cu:1395-1415), so a header whose sections end
+// within 200 bytes of 2^64 yields a packed size below 200, passes
+// `buffer_size < packed_size` and is accepted with sections far outside the
+// buffer; this build rejects it (the only difference from the reference's
+// checks, and only for such headers).
+static bool payload_end_fits(const bitsqz_llm_array_t *c, uint64_t buffer_size) {
+    const bitsqz_section_t secs[6] = {c->section_u, c->section_s, c->section_v, c->section_direct,
+                                      c->section_outlier_topk, c->section_error_topk};
+    for (const auto &s : secs) {
+        if (s.storage == BITSQZ_SECTION_NONE) continue;
+        if (s.offset > UINT64_MAX - s.size) return false;
+        if (s.offset + s.size > buffer_size - sizeof(bitsqz_llm_array_t)) return false;
+    }
+    return true;
+}
+
 bitsqz_llm_array_t *load_bitsqz_llm_from_buffer(const void *buffer, uint64_t buffer_size) {
     if (!buffer || buffer_size < sizeof(bitsqz_llm_array_t)) return nullptr;
     auto *c = static_cast<bitsqz_llm_array_t *>(std::calloc(1, static_cast<size_t>(buffer_size)));
@@ -993,7 +1011,7 @@ bitsqz_llm_array_t *load_bitsqz_llm_from_buffer(const void *buffer, uint64_t buf
     std::memcpy(c, buffer, static_cast<size_t>(buffer_size));
     c->payload = reinterpret_cast<uint8_t *>(c) + sizeof(bitsqz_llm_array_t);
     const uint64_t packed = bitsqz_llm_get_packed_size(c);
-    if (packed == 0 || buffer_size < packed) {
+    if (packed == 0 || buffer_size < packed || !payload_end_fits(c, buffer_size)) {
         std::free(c);
         return nullptr;
     }

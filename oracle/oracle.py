@@ -295,6 +295,48 @@ def parse_packed(buf: bytes) -> Packed:
     return p
 
 
+_U64 = (1 << 64) - 1
+
+
+def section_bounds_ok(offset: int, size: int, storage: int, payload_size: int) -> bool:
+    """validate_section_bounds (src/bitsqz_llm.cu:319-332), u64 operands."""
+    if storage == SECTION_NONE:
+        return size == 0
+    if size == 0 or offset > payload_size or size > payload_size - offset:
+        return False
+    return storage in (SECTION_FP32, SECTION_QUANT, SECTION_TOPK)
+
+
+def packed_size(buf: bytes) -> int:
+    """bitsqz_llm_get_packed_size (src/bitsqz_llm.cu:1395-1415): 200 + the largest
+    offset + size of the non-NONE sections, summed in wrapping u64 arithmetic."""
+    end = 0
+    for i in range(6):
+        off, size, storage = _SEC.unpack_from(buf, 48 + 24 * i)
+        if storage != SECTION_NONE:
+            end = max(end, (off + size) & _U64)
+    return (HEADER_SIZE + end) & _U64
+
+
+def load_accepts(buf: bytes) -> bool:
+    """Whether load_bitsqz_llm_from_buffer accepts `buf` (src/bitsqz_llm.cu:
+    1417-1450: at least a header, packed size within the buffer, every section
+    inside the payload), plus the one check this build adds: the payload end is
+    formed without wrapping and lies inside the buffer (the reference's wrapping
+    sum accepts sections that end within 200 bytes of 2^64)."""
+    n = len(buf)
+    if n < HEADER_SIZE:
+        return False
+    packed = packed_size(buf)
+    if packed == 0 or n < packed:
+        return False
+    payload = (packed - HEADER_SIZE) & _U64
+    secs = [_SEC.unpack_from(buf, 48 + 24 * i) for i in range(6)]
+    if not all(section_bounds_ok(off, size, st, payload) for off, size, st in secs):
+        return False
+    return all(st == SECTION_NONE or off + size <= n - HEADER_SIZE for off, size, st in secs)
+
+
 def mask_pointer(buf: bytes) -> bytes:
     """Packed bytes with the process-address payload pointer (bytes 192-199) zeroed."""
     b = bytearray(buf)

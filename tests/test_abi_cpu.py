@@ -164,3 +164,93 @@ def test_device_thresholds_pinned_against_reference_scan():
     lv = O.nf4_levels()
     assert np.all((t > lv[:-1]) & (t < lv[1:]))
     assert O.nf4_threshold_mismatches(t) == 0
+
+
+def _valid_object() -> bytes:
+    """A well-formed packed object (SVD sections U, S, V as NF4 / FP32 / NF4, an
+    outlier blob), built by the oracle's byte-layout restatement."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(7)
+    rows, cols, q = 16, 24, 4
+    U = rng.standard_normal(rows * q).astype(np.float32)
+    V = rng.standard_normal(cols * q).astype(np.float32)
+    S = np.abs(rng.standard_normal(q)).astype(np.float32)
+    idx = np.tile(np.arange(2, dtype=np.uint16), (rows, 1))
+    val = rng.standard_normal((rows, 2)).astype(np.float32)
+    p = O.Packed(rows, cols, 0.1, 0.0, q, 2, q, O.NF4, O.QUANT_NONE, O.QUANT_NONE, 0b011)
+    p.sections["u"] = (O.SECTION_QUANT, O.pack_quant(O.quant_compress(U, O.NF4)))
+    p.sections["s"] = (O.SECTION_FP32, S.tobytes())
+    p.sections["v"] = (O.SECTION_QUANT, O.pack_quant(O.quant_compress(V, O.NF4)))
+    p.sections["outlier"] = (O.SECTION_TOPK, O.pack_topk(rows, cols, idx, val))
+    return p.to_bytes()
+
+
+def test_load_fuzz_corpus_matches_reference_checks():
+    """Seeded corruptions of a valid object's section table and length: the
+    library's load_bitsqz_llm_from_buffer accepts exactly the buffers that the
+    reference's checks accept (oracle load_accepts restates
+    src/bitsqz_llm.cu:319-332, 1395-1450), reports the same packed size for
+    them, and copies every byte except the re-pointed payload pointer."""
+    from oracle import oracle as O
+    L = B.lib()
+    base = _valid_object()
+    assert O.load_accepts(base)
+    rng = np.random.default_rng(20260101)
+    U64 = (1 << 64) - 1
+    payload = len(base) - 200
+    special = [0, 1, 2, 7, payload - 1, payload, payload + 1, payload // 2, 1 << 32, 1 << 63, U64, U64 - 150,
+               U64 - 199, U64 - 200, U64 - 201, U64 - payload]
+    accepted = rejected = 0
+    for case in range(3000):
+        b = bytearray(base)
+        for _ in range(int(rng.integers(1, 4))):
+            kind = int(rng.integers(0, 5))
+            sec = 48 + 24 * int(rng.integers(0, 6))
+            if kind == 0:    # offset
+                v = special[int(rng.integers(len(special)))] if rng.random() < 0.6 else int(rng.integers(0, 2 * payload))
+                struct.pack_into("<Q", b, sec, v & U64)
+            elif kind == 1:  # size
+                v = special[int(rng.integers(len(special)))] if rng.random() < 0.6 else int(rng.integers(0, 2 * payload))
+                struct.pack_into("<Q", b, sec + 8, v & U64)
+            elif kind == 2:  # storage kind
+                b[sec + 16] = int(rng.choice([0, 1, 2, 3, 4, 255]))
+            elif kind == 3:  # length
+                cut = int(rng.integers(-64, 65))
+                b = b[:max(0, len(b) + cut)] if cut < 0 else b + bytes(cut)
+            else:            # a random byte of the section table
+                b[48 + int(rng.integers(0, 144))] = int(rng.integers(0, 256))
+        buf = bytes(b)
+        want = O.load_accepts(buf)
+        cb = C.create_string_buffer(buf, max(len(buf), 1))
+        p = L.bsq_load_from_buffer(cb, len(buf))
+        assert bool(p) == want, (case, [struct.unpack_from("<QQB", buf, 48 + 24 * i) for i in range(6)]
+                                 if len(buf) >= 192 else len(buf))
+        if p:
+            accepted += 1
+            vp = C.cast(p, C.c_void_p)
+            assert L.bsq_get_packed_size(vp) == O.packed_size(buf)
+            got = C.string_at(vp.value, len(buf))
+            assert O.mask_pointer(got) == O.mask_pointer(buf)
+            assert struct.unpack_from("<Q", got, 192)[0] == vp.value + 200
+            L.bsq_free(vp)
+        else:
+            rejected += 1
+    assert accepted > 100 and rejected > 100, (accepted, rejected)
+
+
+def test_load_rejects_wrapped_payload_end():
+    """A section ending within 200 bytes of 2^64 makes the reference's wrapping
+    packed size fall below 200, so its checks accept a header whose section lies
+    far outside the buffer; this build rejects it (the one intended difference)."""
+    from oracle import oracle as O
+    buf = bytearray(_valid_object())
+    for i in range(6):
+        struct.pack_into("<QQB", buf, 48 + 24 * i, 0, 0, 0)
+    U64 = (1 << 64) - 1
+    struct.pack_into("<QQB", buf, 48, U64 - 150, 100, 1)  # FP32 section at 2^64 - 150
+    buf = bytes(buf)
+    payload = (O.packed_size(buf) - 200) & U64
+    assert O.packed_size(buf) < 200 and O.section_bounds_ok(U64 - 150, 100, 1, payload)
+    assert not O.load_accepts(buf)
+    cb = C.create_string_buffer(buf, len(buf))
+    assert not B.lib().bsq_load_from_buffer(cb, len(buf))
