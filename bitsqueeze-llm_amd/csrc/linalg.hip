@@ -501,23 +501,21 @@ constexpr int kInvPad = 2 * kInvChunk;  // zero entries after d and e
 
 // one elimination step of P (T - lam I) = L U; returns the new dcur.  The
 // multiplier is the quotient num / p from the hardware reciprocal with one
-// correction step (m0 + r0 (num - p m0)); the stored reciprocal of the pivot
-// takes two Newton steps.  A zero pivot is replaced by tiny.
+// correction step (m0 + r0 (num - p m0)).  The pivot itself is stored
+// (zero replaced by tiny): its reciprocal is refined afterwards by all lanes.
 __device__ __forceinline__ double tridl_step(double dcur, double &ecur, double sub, double dn, double en,
-                                             double tiny, double inv_tiny, double *__restrict__ u0inv,
-                                             double *__restrict__ u1, double *__restrict__ u2,
-                                             double *__restrict__ ml, int *__restrict__ piv, int at) {
+                                             double tiny, double *__restrict__ pv, double *__restrict__ u1,
+                                             double *__restrict__ u2, double *__restrict__ ml,
+                                             int *__restrict__ piv, int at) {
     const bool keep = fabs(dcur) >= fabs(sub);
     const double p = keep ? ((dcur == 0.0) ? tiny : dcur) : sub;
     const double num = keep ? sub : dcur;
     const double r0 = __builtin_amdgcn_rcp(p);
     const double m0 = num * r0;
     const double m = fma(r0, fma(-p, m0, num), m0);
-    double rp = fma(r0, fma(-p, r0, 1.0), r0);
-    rp = fma(rp, fma(-p, rp, 1.0), rp);
     piv[at] = keep ? 0 : 1;
     ml[at] = m;
-    u0inv[at] = (fabs(p) < tiny) ? (p < 0.0 ? -inv_tiny : inv_tiny) : rp;
+    pv[at] = p;
     u1[at] = keep ? ecur : dn;
     u2[at] = keep ? 0.0 : en;
     const double ndcur = fma(-m, keep ? ecur : dn, keep ? dn : ecur);
@@ -525,12 +523,23 @@ __device__ __forceinline__ double tridl_step(double dcur, double &ecur, double s
     return ndcur;
 }
 
-// d, e: the tridiagonal in LDS, e[k - 1 ..] and d[k ..] zero (kInvPad entries)
+// 1 / p as the back substitution uses it: the hardware reciprocal and two
+// Newton steps, pivots below tiny replaced by +-tiny
+__device__ __forceinline__ double tridl_pivot_inverse(double p, double tiny, double inv_tiny) {
+    double rp = __builtin_amdgcn_rcp(p);
+    rp = fma(rp, fma(-p, rp, 1.0), rp);
+    rp = fma(rp, fma(-p, rp, 1.0), rp);
+    return (fabs(p) < tiny) ? (p < 0.0 ? -inv_tiny : inv_tiny) : rp;
+}
+
+// d, e: the tridiagonal in LDS, e[k - 1 ..] and d[k ..] zero (kInvPad
+// entries); per-eigenvalue arrays with stride ST
+template <int ST>
 __device__ void tridl_factor(const double *__restrict__ d, const double *__restrict__ e, int k, double lam,
-                             double tiny, double *__restrict__ u0inv, double *__restrict__ u1,
-                             double *__restrict__ u2, double *__restrict__ ml, int *__restrict__ piv, int st) {
+                             double tiny, double *__restrict__ u0inv, double *__restrict__ pv,
+                             double *__restrict__ u1, double *__restrict__ u2, double *__restrict__ ml,
+                             int *__restrict__ piv) {
     constexpr int C = kInvChunk;
-    const double inv_tiny = 1.0 / tiny;
     double dcur = d[0] - lam, ecur = e[0];
     double dq[C], eq[C + 1];  // step i0 + s: d[i0 + 1 + s], e[i0 + s], e[i0 + 1 + s]
 #pragma unroll
@@ -546,8 +555,7 @@ __device__ void tridl_factor(const double *__restrict__ d, const double *__restr
         for (int s = 0; s <= C; ++s) ex[s] = e[i0 + C + s];
 #pragma unroll
         for (int s = 0; s < C; ++s)
-            dcur = tridl_step(dcur, ecur, eq[s], dq[s] - lam, eq[s + 1], tiny, inv_tiny, u0inv, u1, u2, ml, piv,
-                              (i0 + s) * st);
+            dcur = tridl_step(dcur, ecur, eq[s], dq[s] - lam, eq[s + 1], tiny, pv, u1, u2, ml, piv, (i0 + s) * ST);
 #pragma unroll
         for (int s = 0; s < C; ++s) dq[s] = dx[s];
 #pragma unroll
@@ -556,32 +564,26 @@ __device__ void tridl_factor(const double *__restrict__ d, const double *__restr
 #pragma unroll
     for (int s = 0; s < C; ++s)  // fewer than C steps left, operands already staged
         if (i0 + s < k - 1)
-            dcur = tridl_step(dcur, ecur, eq[s], dq[s] - lam, eq[s + 1], tiny, inv_tiny, u0inv, u1, u2, ml, piv,
-                              (i0 + s) * st);
-    u0inv[(k - 1) * st] = 1.0 / ((fabs(dcur) < tiny) ? (dcur < 0.0 ? -tiny : tiny) : dcur);
+            dcur = tridl_step(dcur, ecur, eq[s], dq[s] - lam, eq[s + 1], tiny, pv, u1, u2, ml, piv, (i0 + s) * ST);
+    u0inv[(k - 1) * ST] = 1.0 / ((fabs(dcur) < tiny) ? (dcur < 0.0 ? -tiny : tiny) : dcur);
 }
 
-// Right-hand side of a solve: the start vector of eigenvalue t (START), or
-// the previous iterate b scaled by `scale` as it is read.
-template <bool START>
+// Right-hand side of a solve: the iterate b (stride ST) scaled by `scale` as
+// it is read.
+template <int ST>
 struct InvRhs {
     const double *b;
     double scale;
-    int t, st;
-    __device__ __forceinline__ double operator()(int i) const {
-        if constexpr (START) return start_entry(t, i);
-        else return b[i * st] * scale;
-    }
+    __device__ __forceinline__ double operator()(int i) const { return b[i * ST] * scale; }
 };
 
 // (T - lam I) x = rhs from the factors; x (stride st) may be the array rhs
 // reads.  u1 / u2 must be zero in row k - 1 and u2 in row k - 2.  Returns
 // sum x_i^2.
-template <class Rhs>
+template <int st, class Rhs>
 __device__ double tridl_solve(int k, const double *__restrict__ u0inv, const double *__restrict__ u1,
                               const double *__restrict__ u2, const double *__restrict__ ml,
-                              const int *__restrict__ piv, int st, const Rhs &rhs, double *__restrict__ y,
-                              double *x) {
+                              const int *__restrict__ piv, const Rhs &rhs, double *__restrict__ y, double *x) {
     constexpr int C = kInvChunk;
     // forward elimination rhs -> y (step i: rhs(i + 1), piv[i], ml[i])
     double cur = rhs(0);
@@ -694,43 +696,61 @@ __device__ double tridl_solve(int k, const double *__restrict__ u0inv, const dou
 }
 
 // The same inverse iteration with every per-eigenvalue array in LDS: lane j
-// (< P) of a one-wave workgroup handles eigenvalue blockIdx.x * P + j, its
-// element i at i * P + j.
+// (< P) of a one-wave workgroup runs the recurrences of eigenvalue
+// blockIdx.x * P + j, its element i at i * P + j (P a compile-time stride, so
+// the chunked loads and stores take immediate offsets).  The work off those
+// chains (start vectors, refined pivot reciprocals, the scaled output) is
+// spread over all 64 lanes.
+template <int P>
 __global__ __launch_bounds__(64) void invit_lds_kernel(const double *__restrict__ d, const double *__restrict__ e,
-                                                       int k, int P, const double *__restrict__ lambda,
+                                                       int k, const double *__restrict__ lambda,
                                                        const double *__restrict__ tnorm_p, double *__restrict__ Z) {
     extern __shared__ double sm[];
+    __shared__ double nrm_inv[P];
     const uint64_t kp = static_cast<uint64_t>(k) * P;
     double *u0 = sm, *u1 = u0 + kp, *u2 = u1 + kp, *ml = u2 + kp, *b = ml + kp, *yv = b + kp, *ds = yv + kp,
            *es = ds + k + kInvPad;
     int *piv = reinterpret_cast<int *>(es + k + kInvPad);
-    for (int i = threadIdx.x; i < k + kInvPad; i += blockDim.x) {
+    const int lane = threadIdx.x, t0 = blockIdx.x * P;
+    const double tnorm = fmax(tnorm_p[0], DBL_MIN);
+    const double tiny = tnorm * DBL_EPSILON, inv_tiny = 1.0 / tiny;
+    for (int i = lane; i < k + kInvPad; i += 64) {
         ds[i] = (i < k) ? d[i] : 0.0;
         es[i] = (i + 1 < k) ? e[i] : 0.0;
     }
+    // start vectors; the rows of u1 / u2 the factorisation leaves unwritten but
+    // the back substitution reads (times a zero unknown)
+    for (int q = lane; q < k * P; q += 64) b[q] = start_entry(t0 + q % P, q / P);
+    if (lane < P) {
+        u1[(k - 1) * P + lane] = 0.0;
+        u2[(k - 1) * P + lane] = 0.0;
+        if (k >= 2) u2[(k - 2) * P + lane] = 0.0;
+    }
     __syncthreads();
-    const int j = threadIdx.x, t = blockIdx.x * P + j;
-    if (j >= P || t >= k) return;  // no barrier below
-    const double tnorm = fmax(tnorm_p[0], DBL_MIN);
-    const double tiny = tnorm * DBL_EPSILON;
-    // rows the factorisation leaves unwritten but the back substitution reads
-    // (times a zero unknown)
-    u1[(k - 1) * P + j] = 0.0;
-    u2[(k - 1) * P + j] = 0.0;
-    if (k >= 2) u2[(k - 2) * P + j] = 0.0;
-    tridl_factor(ds, es, k, lambda[t], tiny, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P);
-    // two solves: lambda is within k * eps * ||T|| of the eigenvalue, so one
-    // solve already grows the wanted component by ~1 / (k eps) over components
-    // separated by more than the clustering tolerance (closer ones are redone
-    // by cluster_kernel); the second leaves the iterate at working accuracy.
-    // The first iterate's normalisation is applied as the second solve reads it.
-    const InvRhs<true> start{nullptr, 1.0, t, P};
-    const double n1 = tridl_solve(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, start, yv + j, b + j);
-    const InvRhs<false> again{b + j, n1 > 0.0 ? 1.0 / sqrt(n1) : 0.0, t, P};
-    const double n2 = tridl_solve(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j, P, again, yv + j, b + j);
-    const double inv = n2 > 0.0 ? 1.0 / sqrt(n2) : 0.0;
-    double *z = Z + static_cast<uint64_t>(t) * k;
-    for (int i = 0; i < k; ++i) z[i] = b[i * P + j] * inv;
+    const int j = lane, t = t0 + j;
+    const bool mine = j < P && t < k;
+    if (mine) tridl_factor<P>(ds, es, k, lambda[t], tiny, u0 + j, yv + j, u1 + j, u2 + j, ml + j, piv + j);
+    __syncthreads();
+    for (int q = lane; q < (k - 1) * P; q += 64) u0[q] = tridl_pivot_inverse(yv[q], tiny, inv_tiny);
+    __syncthreads();
+    if (mine) {
+        // two solves: lambda is within k * eps * ||T|| of the eigenvalue, so one
+        // solve already grows the wanted component by ~1 / (k eps) over components
+        // separated by more than the clustering tolerance (closer ones are redone
+        // by cluster_kernel); the second leaves the iterate at working accuracy.
+        // The first iterate's normalisation is applied as the second solve reads it.
+        const double n1 = tridl_solve<P>(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j, InvRhs<P>{b + j, 1.0},
+                                         yv + j, b + j);
+        const double n2 = tridl_solve<P>(k, u0 + j, u1 + j, u2 + j, ml + j, piv + j,
+                                         InvRhs<P>{b + j, n1 > 0.0 ? 1.0 / sqrt(n1) : 0.0}, yv + j, b + j);
+        nrm_inv[j] = n2 > 0.0 ? 1.0 / sqrt(n2) : 0.0;
+    }
+    __syncthreads();
+    const int np = min(P, k - t0);
+    for (int q = lane; q < np * k; q += 64) {
+        const int jj = q / k, i = q - jj * k;
+        Z[static_cast<uint64_t>(t0 + jj) * k + i] = b[i * P + jj] * nrm_inv[jj];
+    }
 }
 
 // Re-runs inverse iteration for eigenvalue clusters (gap below
@@ -1035,9 +1055,21 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
     if (P >= 1) {
         const size_t lds = (6 * static_cast<size_t>(k) * P + 2 * (k + kInvPad)) * sizeof(double) +
                            static_cast<size_t>(k) * P * sizeof(int);
-        BSQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(invit_lds_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        invit_lds_kernel<<<static_cast<unsigned>(ceil_div(k, P)), 64, lds, stream>>>(d, e, k, P, lambda, tn, Z);
+        auto launch = [&](auto kernel) {
+            BSQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+            kernel<<<static_cast<unsigned>(ceil_div(k, P)), 64, lds, stream>>>(d, e, k, lambda, tn, Z);
+        };
+        switch (P) {
+            case 1: launch(invit_lds_kernel<1>); break;
+            case 2: launch(invit_lds_kernel<2>); break;
+            case 3: launch(invit_lds_kernel<3>); break;
+            case 4: launch(invit_lds_kernel<4>); break;
+            case 5: launch(invit_lds_kernel<5>); break;
+            case 6: launch(invit_lds_kernel<6>); break;
+            case 7: launch(invit_lds_kernel<7>); break;
+            default: launch(invit_lds_kernel<8>); break;
+        }
     } else {
         invit_kernel<<<static_cast<unsigned>(ceil_div(k, 64)), 64, 0, stream>>>(d, e, k, lambda, tn, Z, scratch,
                                                                                iscratch);
