@@ -913,14 +913,14 @@ __global__ __launch_bounds__(kMsThreads) void multisect_kernel(const double *__r
 
 // Back-transformation with row-wise reflectors H[j][*]: u_t = H_0 ... H_{k-3} z_t.
 // One wave per eigenvector with z in registers (KPL = ceil(k / 64) values
-// per lane); reflector rows are staged through LDS 16 at a time and shared
+// per lane); reflector rows are staged through LDS 32 at a time and shared
 // by the 4 waves of the workgroup; the dot products reduce through DPP.
 template <int KPL>
 __global__ __launch_bounds__(256) void backtransform_rows_kernel(const double *__restrict__ H,
                                                                  const double *__restrict__ tau, int k,
                                                                  const double *__restrict__ Z,
                                                                  float *__restrict__ Uh) {
-    constexpr int RB = 16, NQ = RB * KPL * 64 / 256;  // rows per stage, staged doubles per lane
+    constexpr int RB = 32, NQ = RB * KPL * 64 / 256;  // rows per stage, staged doubles per lane
     __shared__ double hs[2][RB][KPL * 64];
     __shared__ double ts[2][RB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -963,15 +963,33 @@ __global__ __launch_bounds__(256) void backtransform_rows_kernel(const double *_
         const int jl = max(0, j0 - RB + 1);
         const bool more = j0 - RB >= 0;
         if (more) fetch(j0 - RB);
-        for (int rr = 0; rr <= j0 - jl; ++rr) {
-            const double tj = ts[cur][rr];
-            if (tj == 0.0) continue;  // uniform
-            double s = 0.0;
+        // reflectors in pairs: a = H_j (applied first) and b = H_{j-1} need
+        // v_a.z, v_b.z and v_b.v_a, three independent reductions that overlap,
+        // then z -= s_a v_a + s_b v_b with s_b = tau_b (v_b.z - s_a v_b.v_a).
+        // Rows past the stage are zero with tau zero and change nothing, so
+        // every stage runs all RB rows.
+#pragma unroll 2
+        for (int rp = 0; rp < RB; rp += 2) {
+            const double ta = ts[cur][rp], tb = ts[cur][rp + 1];
+            double va[KPL], vb[KPL];
 #pragma unroll
-            for (int m = 0; m < KPL; ++m) s = fma(hs[cur][rr][lane + 64 * m], z[m], s);
-            s = wave_sum_dpp(s) * tj;
+            for (int m = 0; m < KPL; ++m) {
+                va[m] = hs[cur][rp][lane + 64 * m];
+                vb[m] = hs[cur][rp + 1][lane + 64 * m];
+            }
+            double a = 0.0, b = 0.0, c = 0.0;
 #pragma unroll
-            for (int m = 0; m < KPL; ++m) z[m] = fma(-s, hs[cur][rr][lane + 64 * m], z[m]);
+            for (int m = 0; m < KPL; ++m) {
+                a = fma(va[m], z[m], a);
+                b = fma(vb[m], z[m], b);
+                c = fma(vb[m], va[m], c);
+            }
+            a = wave_sum_dpp(a);
+            b = wave_sum_dpp(b);
+            c = wave_sum_dpp(c);
+            const double sa = ta * a, sb = tb * fma(-sa, c, b);
+#pragma unroll
+            for (int m = 0; m < KPL; ++m) z[m] = fma(-sb, vb[m], fma(-sa, va[m], z[m]));
         }
         if (more) put(cur ^ 1);
         __syncthreads();
