@@ -524,19 +524,25 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
         const bool vec_c = ((g.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15u) == 0) &&
                            (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
         constexpr int Q = 32 * BN / 4 / kThreads;  // float4 per thread per pass
+        // the minuend of all four passes is requested at once (one memory
+        // latency for the epilogue instead of one per pass)
+        float4 mvall[4][Q];
+        if (g.minuend && vec_c) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            float4 mv[Q];
-            if (g.minuend && vec_c) {
+            for (int p = 0; p < 4; ++p)
 #pragma unroll
                 for (int q = 0; q < Q; ++q) {
                     const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
                     const int gi = m0 + 32 * p + rr, gj = n0 + 4 * c4;
-                    mv[q] = (gi < g.M && gj + 4 <= g.N)
-                                ? *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj)
-                                : float4{0.f, 0.f, 0.f, 0.f};
+                    mvall[p][q] = (gi < g.M && gj + 4 <= g.N)
+                                      ? *reinterpret_cast<const float4 *>(g.minuend +
+                                                                         static_cast<uint64_t>(gi) * g.ldc + gj)
+                                      : float4{0.f, 0.f, 0.f, 0.f};
                 }
-            }
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const float4(&mv)[Q] = mvall[p];
             __syncthreads();  // the ring (p = 0) or the previous pass is consumed
             if (wm0 == 64 * (p / 2)) {
 #pragma unroll
