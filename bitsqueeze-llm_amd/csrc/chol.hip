@@ -1,18 +1,17 @@
 // Blocked Cholesky factorisation and triangular inverse for CholeskyQR
 // (k x k FP64 Gram matrices, k <= 256).
 //
-//   chol_blocked_kernel   one workgroup of 1024 lanes; the lower triangle of
-//                         the padded KP x KP matrix (KP = 32 * NB) lives in
-//                         registers, lane (ty, tx) holding element
-//                         (32a + ty, 32b + tx) of every lower 32 x 32 block.
-//                         Right-looking by 32-column panels: one wave
-//                         factors and inverts the diagonal block, all lanes
-//                         form the panel L_ij = A_ij L_jj^{-T} and apply the
-//                         rank-32 trailing update from an LDS copy of the
-//                         panel.  8 panel steps replace 256 column steps, so
-//                         the workgroup synchronises ~50 times instead of
-//                         ~1500.  Breakdown (pivot <= 1e-15 max|G_ii|) restarts
-//                         with a diagonal shift, as the unblocked version does.
+//   chol_blocked_kernel   one workgroup of 1024 lanes.  Waves 1..15 hold the
+//                         lower 16 x 16 tiles of the padded KP x KP matrix
+//                         (KP = 32 * NB) in MFMA accumulator layout; wave 0
+//                         factors and inverts the 32 x 32 diagonal blocks.
+//                         Right-looking by 32-column panels with look-ahead:
+//                         the panel solve L_ij = A_ij L_jj^{-T} and the rank-32
+//                         trailing update run on the FP64 matrix cores, and
+//                         wave 0 factors block j + 1 while the other waves
+//                         finish the trailing update of step j.  Breakdown
+//                         (pivot <= 1e-15 max|G_ii|) restarts with a diagonal
+//                         shift, as the unblocked version does.
 //   trinv_kernel          L^{-1} by blocked forward substitution on the FP64
 //                         matrix cores, 16 columns per workgroup, so the
 //                         inverse is spread over k / 16 CUs.  Writes B = L^{-T} in
@@ -83,10 +82,165 @@ __device__ double wg_max(double v, double *red) {
     return s;
 }
 
-// Lout: KP x KP row-major (lower blocks written: L; diagonal blocks with
-// zeros above the diagonal).  LIout: NB blocks of 32 x 32, the inverses of
-// the diagonal blocks of L (zeros above the diagonal).  status[0]: number of
-// shifted restarts (7 = gave up, L = I).
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// Lower 16 x 16 tile number idx of an NT x NT tile grid, tiles ordered by
+// column, then row: column J starts at J NT - J (J - 1) / 2.
+template <int NT>
+__device__ __forceinline__ void tile_coords(int idx, int &I, int &J) {
+    int j = 0;
+#pragma unroll
+    for (int t = 1; t < NT; ++t) j = (idx >= t * NT - t * (t - 1) / 2) ? t : j;
+    J = j;
+    I = j + idx - (j * NT - j * (j - 1) / 2);
+}
+
+// Cholesky factor and inverse of the 16 x 16 block S[0..16)[0..16) (lower
+// triangle used) on one wave: 8 x 8 lane grid, lane (lr, lc) holding the 2 x 2
+// sub-blocks a = A[2lr.., 2lc..] and x = X[2lr.., 2lc..] of the block and of
+// its inverse (X starts as I).  Step t: scale column t of A and row t of X by
+// 1/sqrt(pivot), fetch the two column-t values of this lane's rows and
+// columns and the two row-t values of X with lane permutes, then rank-1
+// update A's trailing columns and X's trailing rows (Gauss-Jordan on [L | I]
+// fused into the factorisation).  Writes L^{-1} (zeros above the diagonal) to
+// LIo; returns true when a pivot is <= tiny (or NaN).
+template <int PITCH>
+__device__ __forceinline__ bool gj_factor16(const double (*S)[PITCH], double (*LIo)[PITCH], double tiny, int lane) {
+    const int lr = lane >> 3, lc = lane & 7;
+    double a[2][2], x[2][2];
+    const double on_diag = static_cast<double>(1u - min(1u, static_cast<unsigned>(lr ^ lc)));
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            a[p][q] = S[2 * lr + p][2 * lc + q];
+            x[p][q] = (p == q) ? on_diag : 0.0;
+        }
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int tb = t >> 1, tq = t & 1;
+        const double dtt = lane_value(a[tq][tq], tb * 9);
+        bad = bad || !(dtt > tiny);
+        const double inv = rsqrt(dtt);
+        const double fc = (lc == tb) ? inv : 1.0, fr = (lr == tb) ? inv : 1.0;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) a[p][tq] *= fc;  // column t of L (row t: sqrt(pivot))
+#pragma unroll
+        for (int q = 0; q < 2; ++q) x[tq][q] *= fr;  // row t of L^{-1}
+        double lrow[2], lcol[2], xrow[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            lrow[p] = lane_fetch(a[p][tq], lr * 8 + tb);  // L[2lr + p][t]
+            lcol[p] = lane_fetch(a[p][tq], lc * 8 + tb);  // L[2lc + p][t]
+            xrow[p] = lane_fetch(x[tq][p], tb * 8 + lc);  // X[t][2lc + p]
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            // only columns c > t of A and rows i > t of X change; the lower
+            // triangle of A is all that feeds L
+            const double cb = keep_if(lcol[p], static_cast<unsigned>(t - (2 * lc + p)) >> 31);
+            const double rb = keep_if(lrow[p], static_cast<unsigned>(t - (2 * lr + p)) >> 31);
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                a[q][p] = fma(-lrow[q], cb, a[q][p]);
+                x[p][q] = fma(-rb, xrow[q], x[p][q]);
+            }
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) LIo[2 * lr + p][2 * lc + q] = x[p][q];
+    return bad;
+}
+
+// Factors the 32 x 32 diagonal block in Dg (lower triangle used) on one wave
+// and writes its inverse to LI (zeros above the diagonal) and to LIblk, by
+// 2 x 2 blocks of 16:
+//   L11, L11^{-1} = gj_factor16(A11);   L21 = A21 L11^{-T};
+//   L22, L22^{-1} = gj_factor16(A22 - L21 L21^T);
+//   (L^{-1})21 = -L22^{-1} (L21 L11^{-1}).
+// The four 16 x 16 products run on the matrix cores (four dependent
+// 16 x 16 x 4 steps each); Dg's upper right quarter (unused by the lower
+// triangle) and, once factored, its upper left quarter stage the transposes.
+// MFMA operand lanes: A[r][q] and B[q][c] in lane 16 q + (r or c);
+// accumulator register u of lane l holds D[4 u + l / 16][l % 16].
+// Returns true when a pivot is <= tiny (or NaN).
+template <int PITCH>
+__device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*LI)[PITCH],
+                                                  double *__restrict__ LIblk, double tiny, int lane) {
+    const int kq = lane >> 4, cc = lane & 15;
+    bool bad = gj_factor16<PITCH>(Dg, LI, tiny, lane);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) LI[4 * u + kq][16 + cc] = 0.0;
+    wave_lds_fence();
+    // L21 = A21 L11^{-T}: A = Dg[16 + r][k], B[k][c] = LI[c][k]  -> Dg[r][16 + c]
+    f64x4 t = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        t = __builtin_amdgcn_mfma_f64_16x16x4f64(Dg[16 + cc][4 * s + kq], LI[cc][4 * s + kq], t, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) Dg[4 * u + kq][16 + cc] = t[u];
+    wave_lds_fence();
+    // A22 -= L21 L21^T: A[r][k] = -L21[r][k], B[k][c] = L21[c][k]
+#pragma unroll
+    for (int u = 0; u < 4; ++u) t[u] = Dg[16 + 4 * u + kq][16 + cc];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        t = __builtin_amdgcn_mfma_f64_16x16x4f64(-Dg[cc][16 + 4 * s + kq], Dg[cc][16 + 4 * s + kq], t, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) Dg[16 + 4 * u + kq][16 + cc] = t[u];
+    wave_lds_fence();
+    // T = L21 L11^{-1} (A[r][k] = L21[r][k], B[k][c] = LI[k][c]) -> Dg[r][c]
+    // (A11 is no longer needed)
+    t = f64x4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        t = __builtin_amdgcn_mfma_f64_16x16x4f64(Dg[cc][16 + 4 * s + kq], LI[4 * s + kq][cc], t, 0, 0, 0);
+    bad = gj_factor16<PITCH>(reinterpret_cast<const double (*)[PITCH]>(&Dg[16][16]),
+                             reinterpret_cast<double (*)[PITCH]>(&LI[16][16]), tiny, lane) || bad;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) Dg[4 * u + kq][cc] = t[u];
+    wave_lds_fence();
+    // (L^{-1})21 = -L22^{-1} T: A[r][k] = -LI[16 + r][16 + k], B[k][c] = T[k][c]
+    t = f64x4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        t = __builtin_amdgcn_mfma_f64_16x16x4f64(-LI[16 + cc][16 + 4 * s + kq], Dg[4 * s + kq][cc], t, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) LI[16 + 4 * u + kq][cc] = t[u];
+    wave_lds_fence();
+    // LI -> LIblk (32 x 32 row-major): 16 doubles per lane
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int e = 64 * u + lane, r = e >> 5, c = e & 31;
+        LIblk[e] = LI[r][c];
+    }
+    return bad;
+}
+
+// Lout: KP x KP row-major, the blocks below the diagonal blocks written (the
+// triangular inverse reads nothing else).  LIout: NB blocks of 32 x 32, the
+// inverses of the diagonal blocks of L (zeros above the diagonal).
+// status[0]: number of shifted restarts (7 = gave up, L = I).
+//
+// Right-looking by 32-column panels with look-ahead.  Wave 0 only factors the
+// diagonal blocks (factor_diag_block).  Waves 1..15 hold the lower 16 x 16
+// tiles (I >= J) of the padded matrix in the accumulator layout of
+// v_mfma_f64_16x16x4f64 (register u of lane l holds tile element
+// (4u + l / 16, l % 16)), ordered by column then row, wave w owning tiles
+// w - 1, w + 14, w + 29, ...; every trailing matrix is a suffix of that order,
+// so each step's tiles are spread over the 15 waves to within one.  Step jb:
+//   B1  wave 0 has factored block jb (LI);
+//       panel L_I,jb = A_I,jb L_jj^{-T} on the matrix cores (A from the LDS
+//       panel X, result to the LDS panel Y and to Lout);
+//   B2  the diagonal block jb + 1 takes its update A -= L L^T first and goes
+//       to Dg;
+//   B3  wave 0 factors block jb + 1 while waves 1..15 update the rest of the
+//       trailing matrix and copy the next panel into X.
+// The products read their operands from LDS: two 8-byte reads per
+// 16 x 16 x 4 product.
 template <int NB>
 __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double *__restrict__ G, int k,
                                                                      double *__restrict__ Lout,
@@ -94,11 +248,16 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
                                                                      int *__restrict__ status,
                                                                      const int *__restrict__ run) {
     if (run && run[0] == 0) return;  // uniform: the refinement step replaced this pass
-    constexpr int KP = NB * 32, NE = NB * (NB + 1) / 2, PR = (NB > 1) ? (NB - 1) * 32 : 1;
-    __shared__ double Dg[32][33];                          // diagonal block (row-major)
-    __shared__ __attribute__((aligned(16))) double LI[32][34];  // L_jj^{-1}, row-major
-    __shared__ __attribute__((aligned(16))) double P[PR][34];   // panel rows below the diagonal block
-    __shared__ double stash[NE][64];                       // wave 0's registers during its solo phase
+    constexpr int KP = NB * 32, NT = 2 * NB, NTILES = NT * (NT + 1) / 2;
+    constexpr int TW = kCholThreads / 64 - 1, SLOTS = (NTILES + TW - 1) / TW;
+    constexpr int PR = (NB > 1) ? (NB - 1) * 32 : 1;
+    // pitch 33 (odd): the MFMA operand reads (16 rows, one column each) and the
+    // tile stores (one row, 16 columns) hit 32 distinct banks per 16 lanes
+    constexpr int PITCH = 33;
+    __shared__ double Dg[32][PITCH];  // diagonal block: its three lower 16 x 16 tiles
+    __shared__ double LI[32][PITCH];  // L_jj^{-1}, zeros above the diagonal
+    __shared__ double X[PR][PITCH];   // panel rows below the diagonal block, before the solve
+    __shared__ double Y[PR][PITCH];   // the same rows of L
     __shared__ double red[kCholThreads / 64];
     __shared__ int broke;
 
@@ -106,148 +265,149 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
     for (int i = threadIdx.x; i < k; i += kCholThreads) dmax = fmax(dmax, fabs(G[static_cast<uint64_t>(i) * k + i]));
     dmax = wg_max(dmax, red);
     const double tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     double shift = 0.0;
     int attempt = 0;
     bool identity = false;
-    double r[NE];
     for (;; ++attempt) {
-        int tid = opaque(static_cast<int>(threadIdx.x));
-        int tx = tid & 31, ty = tid >> 5;
-#pragma unroll
-        for (int a = 0; a < NB; ++a)
-#pragma unroll
-            for (int b = 0; b <= a; ++b) {
-                // branch-free: G (+ shift on the diagonal) inside, identity in the padding
-                const int i = a * 32 + ty, c = b * 32 + tx;
-                const unsigned inside = (static_cast<unsigned>(i - k) >> 31) & (static_cast<unsigned>(c - k) >> 31);
-                const unsigned diag = 1u - min(1u, static_cast<unsigned>(i ^ c));
-                const double g = G[inside ? static_cast<uint64_t>(i) * k + c : 0];
-                r[tri(a, b)] = keep_if(g, inside) +
-                               static_cast<double>(diag) * (inside ? shift : 1.0);
-            }
-        if (tid == 0) broke = 0;
+        if (threadIdx.x == 0) broke = 0;
         bool failed = false;
+        if (wave == 0) {
+            // the factorisation wave (issued first on its SIMD: it is the
+            // critical path); the same barrier sequence as the tile waves
+            __builtin_amdgcn_s_setprio(3);
+            __syncthreads();  // P0: block 0 is in Dg
+#pragma unroll 1
+            for (int jb = 0; jb < NB; ++jb) {
+                const int lane = opaque(static_cast<int>(threadIdx.x)) & 63;
+                const bool bad = factor_diag_block<PITCH>(Dg, LI, LIout + static_cast<uint64_t>(jb) * 1024, tiny, lane);
+                if (bad && lane == 0) broke = 1;
+                __syncthreads();  // B1
+                if (broke) {
+                    failed = true;
+                    break;
+                }
+                if (jb + 1 < NB) {
+                    __syncthreads();  // B2
+                    __syncthreads();  // B3
+                }
+            }
+            __builtin_amdgcn_s_setprio(0);
+        } else {
+            int tI[SLOTS], tJ[SLOTS];
 #pragma unroll
-        for (int jb = 0; jb < NB; ++jb) {
-            if (failed) break;
-            tid = opaque(static_cast<int>(threadIdx.x));
-            tx = tid & 31;
-            ty = tid >> 5;
-            const int lane = tid & 63, wave = tid >> 6;
-            __syncthreads();  // readers of Dg / P from the previous step are done
-            Dg[ty][tx] = r[tri(jb, jb)];
+            for (int m = 0; m < SLOTS; ++m) {
+                const int idx = TW * m + wave - 1;
+                tile_coords<NT>(idx < NTILES ? idx : 0, tI[m], tJ[m]);
+                if (idx >= NTILES) tJ[m] = -1;  // no tile in this slot
+            }
+            f64x4 acc[SLOTS];
+            {
+                const int lane = opaque(static_cast<int>(threadIdx.x)) & 63, kq = lane >> 4, cc = lane & 15;
 #pragma unroll
-            for (int a = jb + 1; a < NB; ++a) P[(a - jb - 1) * 32 + ty][tx] = r[tri(a, jb)];
-            __syncthreads();
-            if (wave == 0) {
-                // free wave 0's registers for the 32 x 32 factorisation
-#pragma unroll
-                for (int e = 0; e < NE; ++e) stash[e][lane] = r[e];
-                // the compiler may not forward the stash into the reload below (that
-                // would keep r live through the factorisation)
-                asm volatile("" ::: "memory");
-                // 8 x 8 lane grid, lane (lr, lc) holding the 4 x 4 sub-blocks
-                // a = A[4lr.., 4lc..] and x = X[4lr.., 4lc..] of the diagonal
-                // block and of its inverse (X starts as I).  Step t: scale column
-                // t of A and row t of X by 1/sqrt(pivot), fetch the four column-t
-                // values of this lane's rows and columns and the four row-t values
-                // of X with lane permutes, then rank-1 update A's trailing columns
-                // and X's trailing rows (Gauss-Jordan on [L | I] fused into the
-                // factorisation).
-                const int lr = lane >> 3, lc = lane & 7;
-                double a[4][4], x[4][4];
-                const double on_diag = static_cast<double>(1u - min(1u, static_cast<unsigned>(lr ^ lc)));
-#pragma unroll
-                for (int p = 0; p < 4; ++p)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        a[p][q] = Dg[4 * lr + p][4 * lc + q];
-                        x[p][q] = (p == q) ? on_diag : 0.0;
+                for (int m = 0; m < SLOTS; ++m) {
+                    if (tJ[m] < 0) {  // uniform
+                        acc[m] = f64x4{0.0, 0.0, 0.0, 0.0};
+                        continue;
                     }
-                bool bad = false;
+                    // G (+ shift on the diagonal) inside, identity in the padding; the
+                    // loads are clamped into G and masked, so no lane branches
+                    const int c = 16 * tJ[m] + cc;
+                    const unsigned cin = static_cast<unsigned>(c - k) >> 31;
 #pragma unroll
-                for (int t = 0; t < 32; ++t) {
-                    const int tb = t >> 2, tq = t & 3;
-                    const double dtt = lane_value(a[tq][tq], tb * 9);
-                    bad = bad || !(dtt > tiny);
-                    const double inv = rsqrt(dtt);
-                    const double fc = (lc == tb) ? inv : 1.0, fr = (lr == tb) ? inv : 1.0;
-#pragma unroll
-                    for (int p = 0; p < 4; ++p) a[p][tq] *= fc;  // column t of L (row t: sqrt(pivot))
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) x[tq][q] *= fr;  // row t of L^{-1}
-                    double lrow[4], lcol[4], xrow[4];
-#pragma unroll
-                    for (int p = 0; p < 4; ++p) {
-                        lrow[p] = lane_fetch(a[p][tq], lr * 8 + tb);  // L[4lr + p][t]
-                        lcol[p] = lane_fetch(a[p][tq], lc * 8 + tb);  // L[4lc + p][t]
-                        xrow[p] = lane_fetch(x[tq][p], tb * 8 + lc);  // X[t][4lc + p]
+                    for (int u = 0; u < 4; ++u) {
+                        const int i = 16 * tI[m] + 4 * u + kq;
+                        const unsigned inside = (static_cast<unsigned>(i - k) >> 31) & cin;
+                        const unsigned diag = 1u - min(1u, static_cast<unsigned>(i ^ c));
+                        const double g = G[static_cast<unsigned>(min(i, k - 1) * k + min(c, k - 1))];
+                        acc[m][u] = keep_if(g, inside) + static_cast<double>(diag) * (inside ? shift : 1.0);
                     }
+                }
+                // block 0 -> Dg (lower tiles), panel 0 -> X
 #pragma unroll
-                    for (int p = 0; p < 4; ++p) {
-                        // only columns c > t of A and rows i > t of X change
-                        const double cb = keep_if(lcol[p], static_cast<unsigned>(t - (4 * lc + p)) >> 31);
-                        const double rb = keep_if(lrow[p], static_cast<unsigned>(t - (4 * lr + p)) >> 31);
+                for (int m = 0; m < SLOTS; ++m) {
+                    const int I = tI[m], J = tJ[m];
+                    if (J == 0 || J == 1) {
+                        if (I < 2) {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            a[q][p] = fma(-lrow[q], cb, a[q][p]);
-                            x[p][q] = fma(-rb, xrow[q], x[p][q]);
+                            for (int u = 0; u < 4; ++u) {
+                                Dg[16 * I + 4 * u + kq][16 * J + cc] = acc[m][u];
+                            }
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) X[16 * (I - 2) + 4 * u + kq][16 * J + cc] = acc[m][u];
                         }
                     }
                 }
-                if (bad && lane == 0) broke = 1;
-#pragma unroll
-                for (int p = 0; p < 4; ++p)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        LI[4 * lr + p][4 * lc + q] = x[p][q];  // exactly zero above the diagonal
-                        LIout[static_cast<uint64_t>(jb) * 1024 + (4 * lr + p) * 32 + 4 * lc + q] = x[p][q];
-                    }
-                asm volatile("" ::: "memory");
-#pragma unroll
-                for (int e = 0; e < NE; ++e) r[e] = stash[e][lane];
             }
-            __syncthreads();
-            if (broke) {
-                failed = true;
-                break;
-            }
-
-            // panel: L_ij = A_ij L_jj^{-T}, element (32a + ty, 32 jb + tx)
-            double acc[NB];
-#pragma unroll
-            for (int a = 0; a < NB; ++a) acc[a] = 0.0;
+            __syncthreads();  // P0
+            // jb stays a loop: the tile registers are indexed by slot only
 #pragma unroll 1
-            for (int t = 0; t < 32; t += 2) {
-                const double2 li = *reinterpret_cast<const double2 *>(&LI[tx][t]);
-#pragma unroll
-                for (int a = jb + 1; a < NB; ++a) {
-                    const double2 pa = *reinterpret_cast<const double2 *>(&P[(a - jb - 1) * 32 + ty][t]);
-                    acc[a] = fma(pa.x, li.x, fma(pa.y, li.y, acc[a]));
+            for (int jb = 0; jb < NB; ++jb) {
+                const int lane = opaque(static_cast<int>(threadIdx.x)) & 63, kq = lane >> 4, cc = lane & 15;
+                __syncthreads();  // B1: LI holds block jb's inverse
+                if (broke) {
+                    failed = true;
+                    break;
                 }
-            }
-            __syncthreads();  // every lane has read the A panel
+                if (jb + 1 < NB) {
+                    // panel: A[r][q] = X[row r][4s + q], B[q][c] = LI[c][4s + q]
+                    // (LI is lower triangular: its first 16 rows end at column 15)
 #pragma unroll
-            for (int a = jb + 1; a < NB; ++a) {
-                r[tri(a, jb)] = acc[a];
-                P[(a - jb - 1) * 32 + ty][tx] = acc[a];
-                Lout[static_cast<uint64_t>(a * 32 + ty) * KP + jb * 32 + tx] = acc[a];
-            }
-            __syncthreads();
-            // trailing update A_ab -= L_aj L_bj^T for jb < b <= a
-            if (jb + 1 < NB) {
-#pragma unroll 1
-                for (int t = 0; t < 32; t += 2) {  // two panel columns per pass: 16-byte LDS reads
-                    double2 rv[NB];
+                    for (int m = 0; m < SLOTS; ++m) {
+                        const int I = tI[m], J = tJ[m];
+                        if ((J == 2 * jb || J == 2 * jb + 1) && I >= 2 * jb + 2) {
+                            const int pr = 16 * (I - 2 * jb - 2), lc16 = 16 * (J - 2 * jb);
+                            f64x4 t = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-                    for (int a = jb + 1; a < NB; ++a)
-                        rv[a] = *reinterpret_cast<const double2 *>(&P[(a - jb - 1) * 32 + ty][t]);
+                            for (int s = 0; s < 8; ++s)
+                                if (s < 4 || J == 2 * jb + 1)
+                                    t = __builtin_amdgcn_mfma_f64_16x16x4f64(X[pr + cc][4 * s + kq],
+                                                                             LI[lc16 + cc][4 * s + kq], t, 0, 0, 0);
 #pragma unroll
-                    for (int b = jb + 1; b < NB; ++b) {
-                        const double2 cv = *reinterpret_cast<const double2 *>(&P[(b - jb - 1) * 32 + tx][t]);
+                            for (int u = 0; u < 4; ++u) {
+                                Y[pr + 4 * u + kq][lc16 + cc] = t[u];
+                                Lout[static_cast<uint64_t>(16 * I + 4 * u + kq) * KP + 16 * J + cc] = t[u];
+                            }
+                        }
+                    }
+                    __syncthreads();  // B2: Y holds the panel of L
+                    // trailing update A_IJ -= L_I,jb L_J,jb^T (2 jb + 2 <= J <= I):
+                    // first the diagonal block jb + 1, which goes to Dg
+                    const int nb0 = 2 * jb + 2;
 #pragma unroll
-                        for (int a = b; a < NB; ++a)
-                            r[tri(a, b)] = fma(-rv[a].y, cv.y, fma(-rv[a].x, cv.x, r[tri(a, b)]));
+                    for (int m = 0; m < SLOTS; ++m) {
+                        const int I = tI[m], J = tJ[m];
+                        if (J >= nb0 && I < nb0 + 2) {
+                            const int pa = 16 * (I - nb0), pb = 16 * (J - nb0);
+                            f64x4 t = acc[m];
+#pragma unroll
+                            for (int s = 0; s < 8; ++s)
+                                t = __builtin_amdgcn_mfma_f64_16x16x4f64(-Y[pa + cc][4 * s + kq], Y[pb + cc][4 * s + kq],
+                                                                         t, 0, 0, 0);
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                Dg[pa + 4 * u + kq][pb + cc] = t[u];
+                            }
+                        }
+                    }
+                    __syncthreads();  // B3: wave 0 factors block jb + 1 meanwhile
+#pragma unroll
+                    for (int m = 0; m < SLOTS; ++m) {
+                        const int I = tI[m], J = tJ[m];
+                        if (J >= nb0 && I >= nb0 + 2) {
+                            const int pa = 16 * (I - nb0), pb = 16 * (J - nb0);
+                            f64x4 t = acc[m];
+#pragma unroll
+                            for (int s = 0; s < 8; ++s)
+                                t = __builtin_amdgcn_mfma_f64_16x16x4f64(-Y[pa + cc][4 * s + kq], Y[pb + cc][4 * s + kq],
+                                                                         t, 0, 0, 0);
+                            acc[m] = t;
+                            if (J < nb0 + 2) {  // the next panel
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) X[pa - 32 + 4 * u + kq][pb + cc] = t[u];
+                            }
+                        }
                     }
                 }
             }
@@ -289,7 +449,6 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
 // MFMA operand lanes: A[r][q] and B[q][c] in lane 16 q + (r or c);
 // accumulator register u of lane l holds D[4 u + l / 16][l % 16].
 // Output B = L^{-T} (k x k FP32 row-major): B[c][r] = L^{-1}[r][c].
-typedef double f64x4 __attribute__((ext_vector_type(4)));
 constexpr int kTrinvThreads = 1024;
 
 template <int NB>
