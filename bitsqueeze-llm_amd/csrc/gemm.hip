@@ -371,8 +371,10 @@ __device__ __forceinline__ void dma16(const float *g, const float *l) {
 // asm statements keep the compiler from moving LDS accesses across it
 template <int PENDING>
 __device__ __forceinline__ void dma_barrier() {
+    static_assert(PENDING >= 0 && PENDING < 64, "vmcnt has six bits");
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xF70 | PENDING);  // vmcnt(PENDING), expcnt/lgkmcnt untouched
+    // vmcnt(PENDING) (bits 3:0 and 15:14), expcnt/lgkmcnt untouched
+    __builtin_amdgcn_s_waitcnt(0xF70 | (PENDING & 15) | ((PENDING >> 4) << 14));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
@@ -474,14 +476,47 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
         }
     };
     const int kk = lane >> 4, cc = lane & 15;
+    // RECON: the minuend of the output tile (four 32-row passes of Q float4
+    // per thread) is requested right after the last operand slice, so it
+    // arrives while the last slices are multiplied.  Every lane issues all
+    // kMv loads (addresses clamped into the matrix), so the waits below can
+    // count them.
+    constexpr int Q = 32 * BN / 4 / kThreads;
+    constexpr int kMv = RECON ? 4 * Q : 0;
+    float4 mvall[4][Q];
+    const bool vec_c = RECON && ((g.ldc & 3) == 0) &&
+                       ((reinterpret_cast<uintptr_t>(g.C + static_cast<uint64_t>(blockIdx.z) * g.split_stride) & 15u) == 0) &&
+                       (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
+    const bool mv_on = RECON && g.minuend && vec_c && g.N >= 4;
+    auto issue_minuend = [&]() {
+        asm volatile("" ::: "memory");  // stays behind the last slice's DMA
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
+                const int gi = min(m0 + 32 * p + rr, g.M - 1), gj = min(n0 + 4 * c4, g.N - 4);
+                mvall[p][q] = *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj);
+            }
+        asm volatile("" ::: "memory");
+    };
     // slice j sits in stage j % 4: cur holds it, nxt (= stage (j + 3) % 4, read
     // in iteration j - 1) receives slice j + 3
     auto body = [&](const float *cur, const float *nxt, int j) {
         const int ahead = min(kStages - 2, nk - 1 - j);  // slices issued after j
-        if (ahead >= 2) dma_barrier<2 * kDmaPerSlice>();
-        else if (ahead == 1) dma_barrier<kDmaPerSlice>();
-        else dma_barrier<0>();
-        if (j + kStages - 1 < nk) issue(nxt, j + kStages - 1);
+        if (mv_on && j + kStages - 1 >= nk) {  // the minuend loads follow the last slice
+            if (ahead >= 2) dma_barrier<2 * kDmaPerSlice + kMv>();
+            else if (ahead == 1) dma_barrier<kDmaPerSlice + kMv>();
+            else dma_barrier<kMv>();
+        } else {
+            if (ahead >= 2) dma_barrier<2 * kDmaPerSlice>();
+            else if (ahead == 1) dma_barrier<kDmaPerSlice>();
+            else dma_barrier<0>();
+        }
+        if (j + kStages - 1 < nk) {
+            issue(nxt, j + kStages - 1);
+            if (mv_on && j + kStages - 1 == nk - 1) issue_minuend();
+        }
         float a[FM][KS], b[FN][KS];
 #pragma unroll
         for (int i = 0; i < FM; ++i) dma_frag<TA, T>(cur, wm0 + i * 16 + cc, kk, a[i]);
@@ -506,6 +541,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
     if (0 < nk) issue(st0, 0);
     if (1 < nk) issue(st1, 1);
     if (2 < nk) issue(st2, 2);
+    if (mv_on && nk <= kStages - 1) issue_minuend();
     for (int j = 0; j < nk; j += kStages) {
         body(st0, st3, j);
         if (j + 1 < nk) body(st1, st0, j + 1);
@@ -521,25 +557,6 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
         // loads; columns are XOR-swizzled by 16 on alternate groups of four
         // rows (the fragment writes of rows r and r + 4 then hit disjoint banks)
         float *Cs = st0;
-        const bool vec_c = ((g.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15u) == 0) &&
-                           (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
-        constexpr int Q = 32 * BN / 4 / kThreads;  // float4 per thread per pass
-        // the minuend of all four passes is requested at once (one memory
-        // latency for the epilogue instead of one per pass)
-        float4 mvall[4][Q];
-        if (g.minuend && vec_c) {
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-#pragma unroll
-                for (int q = 0; q < Q; ++q) {
-                    const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
-                    const int gi = m0 + 32 * p + rr, gj = n0 + 4 * c4;
-                    mvall[p][q] = (gi < g.M && gj + 4 <= g.N)
-                                      ? *reinterpret_cast<const float4 *>(g.minuend +
-                                                                         static_cast<uint64_t>(gi) * g.ldc + gj)
-                                      : float4{0.f, 0.f, 0.f, 0.f};
-                }
-        }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const float4(&mv)[Q] = mvall[p];
@@ -565,7 +582,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
                 float4 v = *reinterpret_cast<const float4 *>(&Cs[rr * BN + ((4 * c4) ^ (16 * ((rr >> 2) & 1)))]);
                 const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
                 if (vec_c && gj + 4 <= g.N) {
-                    if (g.minuend) v = float4{mv[q].x - v.x, mv[q].y - v.y, mv[q].z - v.z, mv[q].w - v.w};
+                    if (mv_on) v = float4{mv[q].x - v.x, mv[q].y - v.y, mv[q].z - v.z, mv[q].w - v.w};
                     *reinterpret_cast<float4 *>(C + e) = v;
                 } else {
                     const float vv[4] = {v.x, v.y, v.z, v.w};

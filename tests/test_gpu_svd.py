@@ -219,6 +219,16 @@ def test_svd_pipeline_config4_like():
     assert rel(O.reconstruct(U, S, V), residual) < 0.2
 
 
+@pytest.mark.parametrize("q", [16, 48, 80])
+def test_svd_pipeline_error_short_rank(q):
+    """The fused reconstruction - residual epilogue with 1, 3 and 5 K-slices
+    (the minuend is requested behind the last operand slice, in the prologue
+    when there are at most three) and a row count that is not a multiple of
+    the 128-row tile."""
+    x = lowrank(200, 1000, 160, 0.8, 0.01, seed=q)
+    check_svd_pipeline(x, 0.0, 0.05, q, 1, B.QUANT_NONE, B.QUANT_NONE)
+
+
 def test_walkthrough_example_8x8():
     """examples/bitsqz_llm_walkthrough.cpp: 8x8 host input, rank 4, NF4 U/V and S."""
     i = np.arange(64)
