@@ -35,8 +35,9 @@ constexpr int kGramTile = 64;
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 constexpr int kGramRows = 32, kGramPitch = kGramTile + 16;  // pitch: 16-bank offset between k rows
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict__ X, int M, int k, int ld,
-                                                         int rows_per_split, bool vec, double *__restrict__ P) {
+                                                         int rows_per_split, double *__restrict__ P) {
     __shared__ __attribute__((aligned(16))) float xi[2][kGramRows][kGramPitch];
     __shared__ __attribute__((aligned(16))) float xj[2][kGramRows][kGramPitch];
     int t = blockIdx.x, ti = 0;
@@ -45,7 +46,6 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
         ++ti;
     }
     const int tj = t;
-    const bool diag = ti == tj;
     const int r0 = blockIdx.y * rows_per_split, r1 = min(M, r0 + rows_per_split);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wi = (wave >> 1) * 32, wj = (wave & 1) * 32;
@@ -56,38 +56,40 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
     struct Stage {
         float4 i[2], j[2];
     };
+    // branch-free loads (row and column clamped into X); the values outside
+    // X are masked to zero only when the chunk goes to LDS, so nothing
+    // consumes a load early and the three chunks of lookahead stay in flight
+    auto load4 = [&](const float *row, int c) -> float4 {
+        if constexpr (VEC) {  // k % 4 == 0: a quad is inside or wholly outside
+            return *reinterpret_cast<const float4 *>(row + min(c, k - 4));
+        } else {
+            return float4{row[min(c, k - 1)], row[min(c + 1, k - 1)], row[min(c + 2, k - 1)], row[min(c + 3, k - 1)]};
+        }
+    };
+    auto mask4 = [&](float4 v, bool rin, int c) -> float4 {
+        v.x = (rin && c < k) ? v.x : 0.0f;
+        v.y = (rin && c + 1 < k) ? v.y : 0.0f;
+        v.z = (rin && c + 2 < k) ? v.z : 0.0f;
+        v.w = (rin && c + 3 < k) ? v.w : 0.0f;
+        return v;
+    };
     auto fetch = [&](int rb, Stage &st) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int lin = tid + 256 * q, rr = lin >> 4, c4 = (lin & 15) * 4;
             const int r = rb + rr, ci = ti * kGramTile + c4, cj = tj * kGramTile + c4;
-            const float *row = X + static_cast<uint64_t>(r) * ld;
-            if (vec && r < r1 && ci + 4 <= k) {
-                st.i[q] = *reinterpret_cast<const float4 *>(row + ci);
-            } else {
-                st.i[q].x = (r < r1 && ci + 0 < k) ? row[ci + 0] : 0.0f;
-                st.i[q].y = (r < r1 && ci + 1 < k) ? row[ci + 1] : 0.0f;
-                st.i[q].z = (r < r1 && ci + 2 < k) ? row[ci + 2] : 0.0f;
-                st.i[q].w = (r < r1 && ci + 3 < k) ? row[ci + 3] : 0.0f;
-            }
-            if (!diag) {
-                if (vec && r < r1 && cj + 4 <= k) {
-                    st.j[q] = *reinterpret_cast<const float4 *>(row + cj);
-                } else {
-                    st.j[q].x = (r < r1 && cj + 0 < k) ? row[cj + 0] : 0.0f;
-                    st.j[q].y = (r < r1 && cj + 1 < k) ? row[cj + 1] : 0.0f;
-                    st.j[q].z = (r < r1 && cj + 2 < k) ? row[cj + 2] : 0.0f;
-                    st.j[q].w = (r < r1 && cj + 3 < k) ? row[cj + 3] : 0.0f;
-                }
-            }
+            const float *row = X + static_cast<uint64_t>(min(r, r1 - 1)) * ld;
+            st.i[q] = load4(row, ci);
+            st.j[q] = load4(row, cj);  // the same columns on diagonal tiles
         }
     };
-    auto put = [&](int b, const Stage &st) {
+    auto put = [&](int b, int rb, const Stage &st) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int lin = tid + 256 * q, rr = lin >> 4, c4 = (lin & 15) * 4;
-            *reinterpret_cast<float4 *>(&xi[b][rr][c4]) = st.i[q];
-            if (!diag) *reinterpret_cast<float4 *>(&xj[b][rr][c4]) = st.j[q];
+            const bool rin = rb + rr < r1;
+            *reinterpret_cast<float4 *>(&xi[b][rr][c4]) = mask4(st.i[q], rin, ti * kGramTile + c4);
+            *reinterpret_cast<float4 *>(&xj[b][rr][c4]) = mask4(st.j[q], rin, tj * kGramTile + c4);
         }
     };
     f64x4 acc[2][2];
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
     const int kk = lane >> 4, cc = lane & 15;
     auto multiply = [&](int b) {
         const float(*BI)[kGramPitch] = xi[b];
-        const float(*BJ)[kGramPitch] = diag ? xi[b] : xj[b];
+        const float(*BJ)[kGramPitch] = xj[b];
 #pragma unroll
         for (int st = 0; st < kGramRows / 4; ++st) {
             const int rr = 4 * st + kk;
@@ -115,25 +117,34 @@ __global__ __launch_bounds__(256) void gram_mfma_kernel(const float *__restrict_
         }
     };
     const int nch = r0 < r1 ? static_cast<int>(ceil_div(r1 - r0, kGramRows)) : 0;
+    // Every step issues the same four loads (chunks past the end read the
+    // clamped last row and are never multiplied), so the compiler's wait
+    // counting sees a fixed ring and waits only for the chunk it stores.
     Stage s0, s1, s2, s3;
-    if (nch > 0) fetch(r0, s0);
-    if (nch > 1) fetch(r0 + kGramRows, s1);
-    if (nch > 2) fetch(r0 + 2 * kGramRows, s2);
-    if (nch > 0) put(0, s0);
+    if (nch > 0) {  // uniform
+        fetch(r0, s0);
+        fetch(r0 + kGramRows, s1);
+        fetch(r0 + 2 * kGramRows, s2);
+        put(0, r0, s0);
+    }
     __syncthreads();
     // chunk c sits in register set c % 4 until it is put into LDS buffer c % 2
     auto step = [&](int c, Stage &ahead, const Stage &next) {
-        if (c + 3 < nch) fetch(r0 + (c + 3) * kGramRows, ahead);
+        fetch(r0 + (c + 3) * kGramRows, ahead);
         multiply(c & 1);
-        if (c + 1 < nch) put((c + 1) & 1, next);
+        put((c + 1) & 1, r0 + (c + 1) * kGramRows, next);
         __syncthreads();
     };
-    for (int c = 0; c < nch; c += 4) {
+    int c = 0;
+    for (; c + 4 <= nch; c += 4) {
         step(c, s3, s1);
-        if (c + 1 < nch) step(c + 1, s0, s2);
-        if (c + 2 < nch) step(c + 2, s1, s3);
-        if (c + 3 < nch) step(c + 3, s2, s0);
+        step(c + 1, s0, s2);
+        step(c + 2, s1, s3);
+        step(c + 3, s2, s0);
     }
+    if (c < nch) step(c, s3, s1);
+    if (c + 1 < nch) step(c + 1, s0, s2);
+    if (c + 2 < nch) step(c + 2, s1, s3);
     double *out = P + static_cast<uint64_t>(blockIdx.y) * k * k;
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -1012,12 +1023,13 @@ void launch_sytrd_blocked(const double *G, int k, double *d, double *e, double *
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-// Row splits of the Gram: about one workgroup per CU over all lower tiles,
-// at least 256 rows each (fewer partial matrices to sum).
+// Row splits of the Gram: at most one workgroup per CU over all lower tiles
+// (rounded down: one CU holding two workgroups would double the kernel's
+// time), at least 256 rows each (fewer partial matrices to sum).
 int gram_splits(int M, int k) {
     const int nt = static_cast<int>(ceil_div(k, kGramTile));
     const int tiles = nt * (nt + 1) / 2;
-    int splits = static_cast<int>(ceil_div(static_cast<uint64_t>(cu_count()), tiles));
+    const int splits = cu_count() / tiles;
     return std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 256))));
 }
 
@@ -1032,8 +1044,9 @@ void launch_gram(const float *X, int M, int k, int ld, double *G, double *worksp
     int splits = gram_splits(M, k);
     const int rows_per = static_cast<int>(ceil_div(ceil_div(M, splits), kGramRows) * kGramRows);
     splits = static_cast<int>(ceil_div(M, rows_per));
-    const bool vec = (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15u) == 0);
-    gram_mfma_kernel<<<dim3(tiles, splits), 256, 0, stream>>>(X, M, k, ld, rows_per, vec, workspace);
+    const bool vec = (ld % 4 == 0) && (k % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15u) == 0);
+    if (vec) gram_mfma_kernel<true><<<dim3(tiles, splits), 256, 0, stream>>>(X, M, k, ld, rows_per, workspace);
+    else gram_mfma_kernel<false><<<dim3(tiles, splits), 256, 0, stream>>>(X, M, k, ld, rows_per, workspace);
     BSQ_HIP(hipGetLastError());
     gram_reduce_kernel<<<static_cast<unsigned>(k), 256, 0, stream>>>(workspace, splits, k, G, rowsq);
     BSQ_HIP(hipGetLastError());
