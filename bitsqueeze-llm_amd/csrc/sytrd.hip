@@ -143,8 +143,10 @@ __global__ __launch_bounds__(kTrdThreads) void sytrd_blocked_kernel(const double
             quad = wave_sum_dpp(quad);
             if (lane == 0) red[wave] = quad;
             __syncthreads();
-            // finish p: four lanes per index, 16 partials each
-            if (tid < 4 * KP) {  // whole waves: 4 KP is a multiple of 128
+            // finish p: four lanes per index, 16 partials each; blocks left
+            // of block jb are skipped (whole waves: 128 lanes per block), the
+            // update reads w only at indices in blocks >= jb
+            if (tid < 4 * KP && (tid >> 7) >= jb) {
                 const int idx = tid >> 2, qq = tid & 3;  // idx = 32 * blk + y
                 const int blk = idx >> 5, y = idx & 31;
                 // this lane's 16 partials: slots 16 m + 4 qq + s
