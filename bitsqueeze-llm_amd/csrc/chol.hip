@@ -502,6 +502,9 @@ __global__ __launch_bounds__(kTrinvThreads) void trinv_kernel(const double *__re
         const int r = t >> 4, j = t & 15;
         X[cb * 32 + r][j] = LIin[static_cast<uint64_t>(cb) * 1024 + r * 32 + co + j];
     }
+    // X is read by other waves: by the first block row's products, or, in the
+    // last column block (no block rows below it), by the output loop directly
+    __syncthreads();
     int at0 = 0;  // first panel piece of step d
 #pragma unroll
     for (int d = 1; d < NB; ++d) {

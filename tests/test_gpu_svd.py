@@ -74,7 +74,10 @@ def test_exact_low_rank_recovery(m, n):
 
 
 @pytest.mark.parametrize("m,n,q,it,decay", [(1024, 2752, 128, 2, 1.2), (2752, 1024, 64, 1, 1.0),
-                                          (777, 1500, 40, 3, 0.8), (600, 600, 100, 0, 1.2)])
+                                          (777, 1500, 40, 3, 0.8), (600, 600, 100, 0, 1.2),
+                                          # ranks that leave padding inside the 16 x 16 tiles of
+                                          # the Cholesky kernel (47) and a single padded block (1)
+                                          (300, 500, 47, 2, 1.2), (90, 64, 1, 2, 1.0)])
 def test_svd_matches_oracle_with_injected_sketch(m, n, q, it, decay):
     A = lowrank(m, n, 512 if min(m, n) > 512 else min(m, n), decay, 0.01, seed=q)
     k = max(1, min(q, m, n))
@@ -112,6 +115,25 @@ def test_svd_zero_and_rank_one():
     x = np.outer(np.arange(1, 65, dtype=np.float32), np.linspace(-1, 1, 96, dtype=np.float32))
     U, S, V = B.svd_lowrank(x, 8, 2)
     assert rel(O.reconstruct(U, S, V), x) < 1e-5
+
+
+def test_svd_rank_one_repeated_between_other_ranks():
+    """Regression: the triangular inverse's last column block (every rank
+    <= 32) read its LDS copy of the diagonal inverse before the other waves
+    had written it, so the rank-one case below came out with an unnormalised
+    basis (S around 1e21) now and then, most often right after a larger-rank
+    call.  Every repetition must give the same factors."""
+    x = np.outer(np.arange(1, 65, dtype=np.float32), np.linspace(-1, 1, 96, dtype=np.float32))
+    rng = np.random.default_rng(0)
+    U0, S0, V0 = B.svd_lowrank(x, 8, 2)
+    assert rel(O.reconstruct(U0, S0, V0), x) < 1e-5
+    for it in range(40):
+        if it % 2:
+            B.svd_lowrank(rng.standard_normal((300, 500)).astype(np.float32), 47, 2)
+        else:
+            B.svd_lowrank(np.zeros((64, 96), np.float32), 8, 2)
+        U, S, V = B.svd_lowrank(x, 8, 2)
+        assert np.array_equal(S, S0) and np.array_equal(U, U0) and np.array_equal(V, V0), it
 
 
 # ------------------------------------------------------------ pipeline ----
