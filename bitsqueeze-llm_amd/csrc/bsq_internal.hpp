@@ -126,6 +126,11 @@ void launch_topk_scatter(const uint16_t *idx0, const float *val0, uint32_t k0,
                          const uint16_t *idx1, const float *val1, uint32_t k1, uint32_t rows,
                          uint32_t cols, float *dense, bool accumulate, hipStream_t stream,
                          const uint32_t *gate0 = nullptr);
+// One list scatter-added at flat positions r * cols + idx (the reference's
+// indexing, for indices >= cols in loaded objects); positions >= rows * cols
+// are skipped.
+void launch_topk_scatter_flat(const uint16_t *idx, const float *val, uint32_t k, uint32_t rows,
+                              uint32_t cols, float *dense, hipStream_t stream);
 
 }  // namespace bsq
 

@@ -816,7 +816,9 @@ __global__ void cluster_kernel(const double *__restrict__ d, const double *__res
 }
 
 // Back-transformation: u_t = H_0 H_1 ... H_{k-3} z_t, one wave per
-// eigenvector; writes Uh[i][t] (FP32, row-major k x k).
+// eigenvector; writes Uh[i][t] (FP32, row-major k x k).  Lane l owns the
+// rows i = l + 64 m for every reflector (entries above the reflector's first
+// row are masked), so each lane only ever reads back its own stores of z.
 __global__ void backtransform_kernel(const double *__restrict__ W, const double *__restrict__ tau, int k,
                                      double *__restrict__ Z, float *__restrict__ Uh) {
     const int lane = threadIdx.x & 63;
@@ -827,14 +829,17 @@ __global__ void backtransform_kernel(const double *__restrict__ W, const double 
         const double tj = tau[j];
         if (tj == 0.0) continue;
         // v has v[0] = 1 at row j+1, then W[j+2.., j]
+        const int i0 = (j + 1) & ~63;  // first 64-row group touching rows >= j+1
         double s = 0.0;
-        for (int i = j + 1 + lane; i < k; i += 64) {
+        for (int i = i0 + lane; i < k; i += 64) {
+            if (i <= j) continue;
             const double vi = (i == j + 1) ? 1.0 : W[static_cast<uint64_t>(i) * k + j];
             s = fma(vi, z[i], s);
         }
         for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
         s *= tj;
-        for (int i = j + 1 + lane; i < k; i += 64) {
+        for (int i = i0 + lane; i < k; i += 64) {
+            if (i <= j) continue;
             const double vi = (i == j + 1) ? 1.0 : W[static_cast<uint64_t>(i) * k + j];
             z[i] -= s * vi;
         }

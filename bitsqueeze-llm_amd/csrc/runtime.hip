@@ -533,7 +533,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
 // Decode into d_dst (src/bitsqz_llm.cu:1304-1393): dense part, then the
 // error top-k, then the outlier top-k, scatter-added in that order.
 void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has_error, float *d_dst,
-                       hipStream_t st, const uint32_t *err_gate = nullptr) {
+                       hipStream_t st, const uint32_t *err_gate = nullptr, bool scatter = true) {
     const bitsqz_llm_array_t &H = P.header;
     const uint32_t rows = H.num_rows, cols = H.num_columns;
     if (H.flags & kFlagSvd) {
@@ -560,9 +560,24 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
                                 P.d_dq_scale[SEC_DIRECT], P.d_codes[SEC_DIRECT], d_dst, st);
         }
     }
+    if (!scatter) return;
     const bool has_outlier = (H.flags & kFlagOutlier) != 0;
     launch_topk_scatter(P.d_topk_idx[1], P.d_topk_val[1], has_error ? P.topk_k[1] : 0, P.d_topk_idx[0],
                         P.d_topk_val[0], has_outlier ? P.topk_k[0] : 0, rows, cols, d_dst, true, st, err_gate);
+}
+
+// True when some index of the host top-k blob at `p` (num_topk_columns per
+// row) is >= cols.  Such an index addresses a later row in the reference's
+// scatter (topk_cuda_utils.cuh:132-149), which the row-local fused scatter
+// does not reproduce.
+bool topk_blob_has_wide_index(const uint8_t *p, uint64_t n, uint32_t cols) {
+    const uint8_t *q = p + sizeof(uint16_t) * 4;
+    uint32_t mx = 0;  // a max-reduction (vectorisable), the blob may be unaligned
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t c = static_cast<uint32_t>(q[2 * i]) | (static_cast<uint32_t>(q[2 * i + 1]) << 8);
+        mx = c > mx ? c : mx;
+    }
+    return n > 0 && mx >= cols;
 }
 
 // ---------------------------------------------------------------------------
@@ -806,7 +821,7 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         stage_section(SEC_DIRECT, c->section_direct, c->quantization_only_format, N, d_dst);
         P.d_dense[SEC_DIRECT] = nullptr;  // already decoded into d_dst
     }
-    bool has_err = false;
+    bool has_err = false, wide = false;
     const bitsqz_section_t *tsec[2] = {&c->section_outlier_topk, &c->section_error_topk};
     const uint32_t tflag[2] = {kFlagOutlier, kFlagError};
     for (int t = 0; t < 2; ++t) {
@@ -826,11 +841,16 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         P.d_topk_val[t] = tb.val;
         P.topk_k[t] = h.num_topk_columns;
         if (t == 1) has_err = true;
+        wide = wide || topk_blob_has_wide_index(pl + tsec[t]->offset, n, cols);
     }
-    if (c->flags & kFlagSvd) {
-        decompress_device(rt, P, has_err, d_dst, st);
-    } else {
-        const bool has_out = (c->flags & kFlagOutlier) != 0;
+    const bool has_out = (c->flags & kFlagOutlier) != 0;
+    if (c->flags & kFlagSvd) decompress_device(rt, P, has_err, d_dst, st, nullptr, !wide);
+    if (wide) {
+        // the reference's two launches: the error set, then the outlier set
+        // (src/bitsqz_llm.cu:1373-1387), each at flat positions
+        if (has_err) launch_topk_scatter_flat(P.d_topk_idx[1], P.d_topk_val[1], P.topk_k[1], rows, cols, d_dst, st);
+        if (has_out) launch_topk_scatter_flat(P.d_topk_idx[0], P.d_topk_val[0], P.topk_k[0], rows, cols, d_dst, st);
+    } else if (!(c->flags & kFlagSvd)) {
         launch_topk_scatter(P.d_topk_idx[1], P.d_topk_val[1], has_err ? P.topk_k[1] : 0, P.d_topk_idx[0],
                             P.d_topk_val[0], has_out ? P.topk_k[0] : 0, rows, cols, d_dst, true, st);
     }

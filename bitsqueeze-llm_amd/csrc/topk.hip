@@ -679,6 +679,21 @@ __global__ __launch_bounds__(256) void topk_scatter_kernel(const uint16_t *__res
     }
 }
 
+// One top-k set at flat positions, as the reference's scatter_add_topk_kernel
+// writes it (topk_cuda_utils.cuh:132-149): dense[r * cols + idx] += v, so an
+// index >= cols lands in a later row.  Used for loaded objects whose indices
+// are not all below cols; positions past the end of the matrix (where the
+// reference would write outside the buffer) are skipped.
+__global__ __launch_bounds__(256) void topk_scatter_flat_kernel(const uint16_t *__restrict__ idx,
+                                                                const float *__restrict__ val, uint32_t k,
+                                                                uint64_t total, uint32_t cols, uint64_t n,
+                                                                float *__restrict__ dense) {
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= total) return;
+    const uint64_t p = (e / k) * cols + idx[e];
+    if (p < n) dense[p] += val[e];
+}
+
 template <TopkSource SRC>
 void launch_src(const TopkArgs &a, hipStream_t stream) {
     if (try_launch_reg<SRC>(a, stream)) return;
@@ -745,6 +760,17 @@ void launch_topk_scatter(const uint16_t *idx0, const float *val0, uint32_t k0, c
         gate0 = nullptr;
     }
     topk_scatter_kernel<<<rows, 256, 0, stream>>>(idx0, val0, k0, idx1, val1, k1, cols, dense, accumulate, gate0);
+    BSQ_HIP(hipGetLastError());
+}
+
+void launch_topk_scatter_flat(const uint16_t *idx, const float *val, uint32_t k, uint32_t rows, uint32_t cols,
+                              float *dense, hipStream_t stream) {
+    BSQ_REQUIRE(rows > 0 && cols > 0 && dense, "top-k scatter: bad arguments");
+    const uint64_t total = static_cast<uint64_t>(rows) * k;
+    if (total == 0) return;
+    BSQ_REQUIRE(idx && val, "top-k scatter: null list");
+    topk_scatter_flat_kernel<<<static_cast<unsigned>(ceil_div(total, 256)), 256, 0, stream>>>(
+        idx, val, k, total, cols, static_cast<uint64_t>(rows) * cols, dense);
     BSQ_HIP(hipGetLastError());
 }
 

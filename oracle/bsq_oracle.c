@@ -203,11 +203,17 @@ ORACLE_API void oracle_nf4dq_compress(const float *x, uint64_t n, float *dq_out,
     free(absmax);
 }
 
-/* NF4_DQ decompress (nf4_dq_impl.cpp:244-275): out = (dq*E4M3^-1(s_b)) * level. */
+/* NF4_DQ decompress (nf4_dq_impl.cpp:244-275): out = (dq*E4M3^-1(s_b)) * level.
+ * The global dq is first replaced by 1 when it is 0 or not finite: the device
+ * decoder on the bitsqz_llm path does that (quantization_cuda.cu:322-325),
+ * the legacy CPU decoder does not; the two agree for every dq the encoders
+ * write (a positive finite value), and only a loaded object can carry
+ * another. */
 ORACLE_API void oracle_nf4dq_decompress(float dq, const uint8_t *scale_codes,
                                         const uint8_t *codes, uint64_t n, float *out) {
     const uint64_t bs = 64, nb = (n + bs - 1) / bs;
     int64_t b;
+    if (dq == 0.0f || !isfinite(dq)) dq = 1.0f;
 #pragma omp parallel for
     for (b = 0; b < (int64_t)nb; ++b) {
         const uint64_t start = (uint64_t)b * bs;

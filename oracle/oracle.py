@@ -514,10 +514,15 @@ def decompress(p: Packed) -> np.ndarray:
         out = reconstruct(U, S, V).astype(np.float32)
     else:
         out = _decode_dense(*p.sections["direct"], p.direct_format, m * n).reshape(m, n)
+    # scatter_add_topk_kernel (topk_cuda_utils.cuh:132-149) writes at the flat
+    # position row * cols + index, so an index >= cols of a loaded object lands
+    # in a later row; positions past the matrix (outside the reference's
+    # buffer) are dropped here
+    flat = out.reshape(-1)
     for name, flag in (("error", FLAG_ERROR), ("outlier", FLAG_OUTLIER)):
         if p.flags & flag:
             _, _, k, idx, val = unpack_topk(p.sections[name][1])
-            rr = np.repeat(np.arange(m), k)
-            cc = idx.ravel().astype(np.int64)
-            np.add.at(out, (rr, cc), val.ravel())
+            pos = np.repeat(np.arange(m, dtype=np.int64), k) * n + idx.ravel().astype(np.int64)
+            keep = pos < m * n
+            np.add.at(flat, pos[keep], val.ravel()[keep])
     return out

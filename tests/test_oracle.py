@@ -253,3 +253,183 @@ def test_pipeline_dense_direct_is_exact():
     p = O.compress(A, O.Config(8, 64, error_ratio=0.1))
     assert p.flags == 0            # dense section: no error extraction
     assert np.array_equal(O.decompress(p), A)
+
+
+# ------------------------------------------------- pipeline composition pins --
+# These pin oracle.compress / oracle.decompress (the restatement of
+# src/bitsqz_llm.cu:981-1393) with checks that do not reuse the oracle's own
+# pipeline code: the top-k is recomputed with numpy's stable sort, and the
+# decoded values are written as explicit float32 operations.  A swapped apply
+# order, an error measured against the raw residual, a `>=` FLT_EPSILON gate
+# or a misplaced section each fail one of them.
+def _stable_topk(err: np.ndarray, k: int):
+    """Per row the k largest |err| (ties to the lower column) by numpy's
+    stable sort: an independent brute force of topk_cuda_utils.cuh:51-93."""
+    key = np.abs(err.astype(np.float32))
+    key = np.where(np.isnan(key), -np.inf, key)
+    order = np.argsort(-key, axis=1, kind="stable")[:, :k]
+    return order.astype(np.uint16), np.take_along_axis(err, order, axis=1).astype(np.float32)
+
+
+def _sections(p: "O.Packed", buf: bytes):
+    """(name -> (offset, size)) read back from the serialized header."""
+    out = {}
+    for i, name in enumerate(O.SECTION_NAMES):
+        off, size, st = struct.unpack_from("<QQB", buf, 48 + 24 * i)
+        if st:
+            out[name] = (off, size, st)
+    return out
+
+
+@pytest.mark.parametrize("method", [O.NF4, O.NF4_DQ])
+def test_composition_direct_error_is_topk_of_residual_minus_dequant(method):
+    """Direct path (src/bitsqz_llm.cu:1183-1227): the error section holds the
+    k_e largest |x - deq(x)| per row, and the decode there is
+    fl(deq + fl(x - deq)) -- the residual minus the *dequantised* section."""
+    rng = np.random.default_rng(21)
+    rows, cols = 12, 320
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    cfg = O.Config(rows, cols, error_ratio=0.05, direct_format=method)
+    ke = O.topk_num_columns(cols, 0.05)
+    p = O.compress(x, cfg)
+    deq = O.quant_decompress(O.quant_compress(x, method)).reshape(rows, cols)
+    err = (x - deq).astype(np.float32)
+    ei, ev = _stable_topk(err, ke)
+    assert p.flags == O.FLAG_ERROR
+    assert p.sections["error"][1] == struct.pack("<HHHH", rows, cols, ke, 0) + ei.tobytes() + ev.tobytes()
+    out = O.decompress(O.parse_packed(p.to_bytes()))
+    expect = deq.copy()
+    for r in range(rows):
+        for j in range(ke):
+            c = int(ei[r, j])
+            expect[r, c] = np.float32(deq[r, c] + np.float32(x[r, c] - deq[r, c]))
+    assert out.tobytes() == expect.tobytes()
+    # section order: direct first, then the error blob, no gaps
+    secs = _sections(p, p.to_bytes())
+    assert secs["direct"][0] == 0 and secs["error"][0] == secs["direct"][1]
+
+
+def test_composition_outliers_are_exact_and_zeroed_before_quantisation():
+    """Outliers are the k_o largest |x| per row; they are zeroed in the
+    residual before the direct section is encoded, and decode to x exactly."""
+    rng = np.random.default_rng(22)
+    rows, cols = 8, 256
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[:, 17] *= 80.0
+    x[3, 200] = -900.0
+    ko = O.topk_num_columns(cols, 0.01)
+    p = O.compress(x, O.Config(rows, cols, outlier_ratio=0.01, error_ratio=0.02, direct_format=O.NF4))
+    oi, ov = _stable_topk(x, ko)
+    assert p.sections["outlier"][1] == struct.pack("<HHHH", rows, cols, ko, 0) + oi.tobytes() + ov.tobytes()
+    residual = x.copy()
+    np.put_along_axis(residual, oi.astype(np.int64), 0.0, axis=1)
+    q = O.quant_compress(residual, O.NF4)
+    assert p.sections["direct"][1] == O.pack_quant(q)
+    out = O.decompress(O.parse_packed(p.to_bytes()))
+    assert np.array_equal(np.take_along_axis(out, oi.astype(np.int64), axis=1), ov)
+    secs = _sections(p, p.to_bytes())
+    assert secs["direct"][0] == 0
+    assert secs["outlier"][0] == secs["direct"][1]
+    assert secs["error"][0] == secs["outlier"][0] + secs["outlier"][1]
+
+
+def test_composition_error_then_outlier_apply_order():
+    """src/bitsqz_llm.cu:1373-1387 adds the error set before the outlier set.
+    Crafted so the two orders round differently: at column 0 the outlier is
+    2^24, the reconstruction 1 and the error -1; error first gives
+    (1 + -1) + 2^24 = 2^24, outlier first gives (1 + 2^24) - 1 = 2^24 - 1."""
+    x = np.ones((1, 8), np.float32)
+    x[0, 0] = np.float32(2.0 ** 24)
+    U = np.ones((1, 1), np.float32)
+    S = np.ones(1, np.float32)
+    V = np.ones((8, 1), np.float32)
+    cfg = O.Config(1, 8, outlier_ratio=0.125, error_ratio=0.125, svd_ranks=1, svd_niters=1)
+    p = O.compress(x, cfg, svd_result=(U, S, V))
+    _, _, ko, oi, ov = O.unpack_topk(p.sections["outlier"][1])
+    _, _, ke, ei, ev = O.unpack_topk(p.sections["error"][1])
+    assert (ko, int(oi[0, 0]), float(ov[0, 0])) == (1, 0, 2.0 ** 24)
+    # the residual is 0 at the outlier, the reconstruction 1: error -1 there
+    assert (ke, int(ei[0, 0]), float(ev[0, 0])) == (1, 0, -1.0)
+    out = O.decompress(O.parse_packed(p.to_bytes()))
+    error_first = np.float32(np.float32(np.float32(1.0) + np.float32(-1.0)) + np.float32(2.0 ** 24))
+    outlier_first = np.float32(np.float32(np.float32(1.0) + np.float32(2.0 ** 24)) + np.float32(-1.0))
+    assert error_first != outlier_first
+    assert out[0, 0] == error_first
+    assert np.all(out[0, 1:] == 1.0)
+
+
+def test_composition_svd_error_uses_dequantised_factors():
+    """With quantised U/V the error is measured against the reconstruction of
+    the *dequantised* factors (src/bitsqz_llm.cu:1078-1163, 506-512)."""
+    rng = np.random.default_rng(23)
+    rows, cols, q = 16, 96, 4
+    U = rng.standard_normal((rows, q)).astype(np.float32)
+    S = np.array([4.0, 3.0, 2.0, 1.0], np.float32)
+    V = rng.standard_normal((cols, q)).astype(np.float32)
+    x = ((U * S) @ V.T).astype(np.float32)
+    cfg = O.Config(rows, cols, error_ratio=0.05, svd_ranks=q, svd_niters=1, uv_format=O.NF4)
+    p = O.compress(x, cfg, svd_result=(U, S, V))
+    du = O.quant_decompress(O.quant_compress(U, O.NF4)).reshape(rows, q).astype(np.float64)
+    dv = O.quant_decompress(O.quant_compress(V, O.NF4)).reshape(cols, q).astype(np.float64)
+    approx = ((du * S.astype(np.float64)) @ dv.T).astype(np.float32)
+    ke = O.topk_num_columns(cols, 0.05)
+    ei, ev = _stable_topk((x - approx).astype(np.float32), ke)
+    assert p.sections["error"][1] == struct.pack("<HHHH", rows, cols, ke, 0) + ei.tobytes() + ev.tobytes()
+    # U, S, V sections in that order at the front of the payload
+    secs = _sections(p, p.to_bytes())
+    assert secs["u"][0] == 0 and secs["s"][0] == secs["u"][1] and secs["v"][0] == secs["s"][0] + secs["s"][1]
+
+
+@pytest.mark.parametrize("bump,present", [(False, False), (True, True)])
+def test_composition_flt_epsilon_gate(bump, present):
+    """The error top-k runs only if some |err| > FLT_EPSILON (strictly;
+    src/bitsqz_llm.cu:175-184, 410).  A block holding 1.0 has scale 1, so an
+    entry of FLT_EPSILON quantises to level 0 and leaves an error of exactly
+    FLT_EPSILON (no error section); the next float up leaves one."""
+    x = np.zeros((2, 64), np.float32)
+    x[:, 0] = 1.0
+    e = np.float32(O.FLT_EPSILON)
+    x[1, 5] = np.nextafter(e, np.float32(1.0)) if bump else e
+    p = O.compress(x, O.Config(2, 64, error_ratio=0.05, direct_format=O.NF4))
+    deq = O.quant_decompress(O.quant_compress(x, O.NF4)).reshape(2, 64)
+    assert deq[1, 5] == 0.0 and np.float32(x[1, 5] - deq[1, 5]) == x[1, 5]
+    assert bool(p.flags & O.FLAG_ERROR) == present
+    assert ("error" in p.sections) == present
+
+
+@pytest.mark.parametrize("dq", [0.0, -0.0, float("nan"), float("inf"), float("-inf"), 1e-45])
+def test_nf4dq_decode_guards_dq_like_the_device_decoder(dq):
+    """quantization_cuda.cu:322-327: a dq of 0 or non-finite decodes as 1;
+    any other value (a subnormal included) is used as it is."""
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal(200).astype(np.float32)
+    q = O.quant_compress(x, O.NF4_DQ)
+    q.dq = dq
+    out = O.quant_decompress(q)
+    eff = np.float32(1.0) if (dq == 0.0 or not math.isfinite(dq)) else np.float32(dq)
+    lv = O.nf4_levels()
+    e4 = O.e4m3_decode_table()
+    expect = np.empty(200, np.float32)
+    for i in range(200):
+        s = np.float32(eff * e4[q.scales[i // 64]])
+        if s == 0.0 or not np.isfinite(s):
+            s = np.float32(1.0)
+        c = (q.codes[i // 2] >> 4) if i % 2 == 0 else (q.codes[i // 2] & 15)
+        expect[i] = np.float32(s * lv[c])
+    assert out.tobytes() == expect.tobytes()
+
+
+def test_decompress_wide_index_flat_position():
+    """An index >= cols adds at row * cols + index (topk_cuda_utils.cuh:
+    132-149); one past the end of the matrix is dropped."""
+    rows, cols = 3, 64
+    p = O.Packed(rows, cols, 1.0 / 64, 0.0, -1, 2, 0, O.QUANT_NONE, O.QUANT_NONE, O.QUANT_NONE, O.FLAG_OUTLIER)
+    p.sections["direct"] = (O.SECTION_FP32, np.zeros(rows * cols, np.float32).tobytes())
+    idx = np.array([[cols + 3], [5], [cols + 1]], np.uint16)
+    val = np.array([[2.5], [4.0], [9.0]], np.float32)
+    p.sections["outlier"] = (O.SECTION_TOPK, O.pack_topk(rows, cols, idx, val))
+    out = O.decompress(O.parse_packed(p.to_bytes()))
+    expect = np.zeros((rows, cols), np.float32)
+    expect[1, 3] = 2.5
+    expect[1, 5] = 4.0
+    assert np.array_equal(out, expect)
