@@ -115,7 +115,8 @@ struct TopkArgs {
     TopkSource source = TopkSource::Dense;
 };
 void launch_topk_select(const TopkArgs &args, hipStream_t stream);
-// Largest k the single-pass LDS sort handles.
+// Largest k the single-workgroup LDS sort handles; larger k (up to the row
+// length) is sorted in bands of this many ranks.
 constexpr uint32_t kTopkMaxK = 8192;
 
 // dense[r, idx[r*k + j]] (+)= val[r*k + j]; with two lists, list 0 is applied

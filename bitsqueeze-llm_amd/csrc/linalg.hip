@@ -230,8 +230,9 @@ __device__ double block_max(double v, double *red) {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kBig) void chol_inv_kernel(const double *__restrict__ G, int k,
                                                          double *__restrict__ W, float *__restrict__ Linv,
-                                                         int *__restrict__ status) {
-    extern __shared__ double col[];  // k doubles
+                                                         int *__restrict__ status, double *__restrict__ col_ext) {
+    extern __shared__ double col_lds[];  // k doubles, or col_ext (global) when they do not fit
+    double *col = col_ext ? col_ext : col_lds;
     __shared__ double red[kBig / 64];
     __shared__ int broke;
     const int tid = threadIdx.x;
@@ -317,8 +318,10 @@ __global__ __launch_bounds__(kBig) void chol_inv_kernel(const double *__restrict
 // tau[j].  One workgroup.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kBig) void sytrd_kernel(double *__restrict__ W, int k, double *__restrict__ d,
-                                                      double *__restrict__ e, double *__restrict__ tau) {
-    extern __shared__ double sm[];  // v[k], p[k]
+                                                      double *__restrict__ e, double *__restrict__ tau,
+                                                      double *__restrict__ vp_ext) {
+    extern __shared__ double sm_lds[];  // v[k], p[k], or vp_ext (global) when they do not fit
+    double *sm = vp_ext ? vp_ext : sm_lds;
     double *v = sm, *p = sm + k;
     __shared__ double red[kBig / 64];
     const int tid = threadIdx.x;
@@ -853,21 +856,33 @@ __global__ void backtransform_kernel(const double *__restrict__ W, const double 
 // recurrence, so a pass costs one count's latency however many lanes share
 // it, and more lanes mean fewer passes.  lambda[t] = t-th largest eigenvalue.
 constexpr int kMsThreads = 256;
+// e2[i] = e[i]^2 (i < k - 1), 0 for i = k - 1: the squared off-diagonal read
+// from global memory by multisect_kernel when d and e2 do not fit in LDS.
+__global__ void square_offdiag_kernel(const double *__restrict__ e, int k, double *__restrict__ e2) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < k) e2[i] = (i + 1 < k) ? e[i] * e[i] : 0.0;
+}
+
+template <bool GLOBAL>
 __global__ __launch_bounds__(kMsThreads) void multisect_kernel(const double *__restrict__ d,
                                                                const double *__restrict__ e, int k,
                                                                double *__restrict__ lambda,
-                                                               double *__restrict__ tnorm_out) {
-    extern __shared__ double sm[];  // d[k], e2[k]
-    double *sd = sm, *se2 = sm + k;
+                                                               double *__restrict__ tnorm_out,
+                                                               const double *__restrict__ e2g) {
+    extern __shared__ double sm[];  // d[k], e2[k] (LDS variant)
+    double *sd = GLOBAL ? const_cast<double *>(d) : sm;
+    double *se2 = GLOBAL ? const_cast<double *>(e2g) : sm + k;
     constexpr int W = kMsThreads / 64;
     __shared__ double red[3][W];
     __shared__ unsigned long long masks[W];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     double lo = 1e300, hi = -1e300, emax = 0.0;
     for (int i = tid; i < k; i += kMsThreads) {
-        sd[i] = d[i];
         const double ei = (i + 1 < k) ? e[i] : 0.0;
-        se2[i] = ei * ei;
+        if (!GLOBAL) {
+            sd[i] = d[i];
+            se2[i] = ei * ei;
+        }
         const double r = (i > 0 ? fabs(e[i - 1]) : 0.0) + fabs(ei);
         lo = fmin(lo, d[i] - r);
         hi = fmax(hi, d[i] + r);
@@ -1058,31 +1073,55 @@ void launch_gram(const float *X, int M, int k, int ld, double *G, double *worksp
 }
 
 // Unblocked fallback for ranks above the blocked kernel's range (k > 256).
-void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(k) * sizeof(double);
-    BSQ_REQUIRE(lds <= 64 * 1024, "chol_inv: rank too large");
-    chol_inv_kernel<<<1, kBig, lds, stream>>>(G, k, W, Linv, status);
+// Dynamic LDS for `bytes` of per-launch vectors: the byte count when it fits
+// beside the kernel's static LDS (raising the launch limit above 64 KiB),
+// else 0 and the caller passes a global buffer instead.
+size_t dyn_lds_or_zero(const void *kernel, size_t bytes) {
+    constexpr size_t kLdsCap = 160 * 1024 - 2048;  // static LDS of these kernels stays below 2 KiB
+    if (bytes > kLdsCap) return 0;
+    if (bytes > 64 * 1024)
+        BSQ_HIP(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+    return bytes;
+}
+
+void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, double *ext, hipStream_t stream) {
+    const size_t lds = dyn_lds_or_zero(reinterpret_cast<const void *>(chol_inv_kernel),
+                                       static_cast<size_t>(k) * sizeof(double));
+    chol_inv_kernel<<<1, kBig, lds, stream>>>(G, k, W, Linv, status, lds ? nullptr : ext);
     BSQ_HIP(hipGetLastError());
 }
 
 // Eigen-decomposition of the symmetric G (k x k FP64): lambda descending,
 // Uh[i][t] = component i of eigenvector t (FP32).  `W` k*k doubles, `Z`
-// k*k doubles, `small` >= 4k + 8 doubles, `scratch` 9*k*k doubles,
+// k*k doubles, `small` >= 4k + 8 doubles, `scratch` 9*k*k + 2k doubles,
 // `iscratch` 2*k*k ints.
 void launch_syev(const double *G, int k, double *W, double *Z, double *small, double *scratch, int *iscratch,
                  double *lambda, float *Uh, hipStream_t stream) {
-    BSQ_REQUIRE(k >= 1 && static_cast<size_t>(2 * k) * sizeof(double) <= 64 * 1024, "syev: rank too large");
+    BSQ_REQUIRE(k >= 1, "syev: empty matrix");
     double *d = small, *e = small + k, *tau = small + 2 * k, *tn = small + 3 * k;
+    // global stand-ins for LDS vectors that do not fit (ranks above ~10000):
+    // the last 2k doubles of the scratch, which the inverse-iteration kernels
+    // below leave alone (they use 5k^2 + 4k^2 of its 9k^2 + 2k doubles)
+    double *ext = scratch + 9ull * k * k;
+    const size_t kb = static_cast<size_t>(k) * sizeof(double);
     bool reg = true;
     if (sytrd_blocked_supported(k)) {
         launch_sytrd_blocked(G, k, d, e, tau, W, stream);
     } else {
         reg = false;
         BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));
-        sytrd_kernel<<<1, kBig, 2 * k * sizeof(double), stream>>>(W, k, d, e, tau);
+        const size_t lds = dyn_lds_or_zero(reinterpret_cast<const void *>(sytrd_kernel), 2 * kb);
+        sytrd_kernel<<<1, kBig, lds, stream>>>(W, k, d, e, tau, lds ? nullptr : ext);
     }
     BSQ_HIP(hipGetLastError());
-    multisect_kernel<<<k, kMsThreads, 2 * k * sizeof(double), stream>>>(d, e, k, lambda, tn);
+    const size_t ms_lds = dyn_lds_or_zero(reinterpret_cast<const void *>(multisect_kernel<false>), 2 * kb);
+    if (ms_lds) {
+        multisect_kernel<false><<<k, kMsThreads, ms_lds, stream>>>(d, e, k, lambda, tn, nullptr);
+    } else {
+        square_offdiag_kernel<<<static_cast<unsigned>(ceil_div(k, 256)), 256, 0, stream>>>(e, k, ext);
+        BSQ_HIP(hipGetLastError());
+        multisect_kernel<true><<<k, kMsThreads, 0, stream>>>(d, e, k, lambda, tn, ext);
+    }
     BSQ_HIP(hipGetLastError());
     // eigenvalues per workgroup whose LDS arrays fit: (6kP + 2(k + pad)) doubles + kP ints
     const int64_t lds_cap = 160 * 1024;

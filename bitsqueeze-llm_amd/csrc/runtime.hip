@@ -247,7 +247,6 @@ namespace {
 void init_topk(TopkBuf &t, uint16_t rows, uint16_t cols, float ratio) {
     t.capacity = topk_num_columns(cols, ratio);
     if (t.capacity == 0) return;
-    BSQ_REQUIRE(t.capacity <= kTopkMaxK, "top-k: k above the supported maximum (8192)");
     const uint64_t n = static_cast<uint64_t>(rows) * t.capacity;
     t.idx = dev_alloc<uint16_t>(n);
     t.val = dev_alloc<float>(n);

@@ -29,7 +29,7 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
 uint64_t gram_workspace_bytes(int M, int k);
 void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream,
                  double *rowsq = nullptr);
-void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, hipStream_t stream);
+void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, double *ext, hipStream_t stream);
 uint64_t chol_blocked_buffer_doubles(int k);
 bool chol_blocked_supported(int k);
 void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream,
@@ -245,7 +245,6 @@ SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
         p->Mw = p->transposed ? n : m;
         p->Nw = p->transposed ? m : n;
         const uint64_t k = p->k;
-        BSQ_REQUIRE(k <= 4096, "svd: rank above the supported maximum (4096)");
         p->R = alloc<float>(p->Nw * k);
         p->X = alloc<float>(p->Mw * k);
         p->X2 = alloc<float>(p->Mw * k);
@@ -263,7 +262,7 @@ SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
         p->csum = alloc<double>(kColChunks * k);
         p->rowsq = alloc<double>(k);
         p->csign = alloc<float>(2 * k);
-        p->scratch = alloc<double>(9 * k * k);
+        p->scratch = alloc<double>(9 * k * k + 2 * k);
         p->lambda = alloc<double>(k);
         p->iscratch = alloc<int>(2 * k * k);
         p->status = alloc<int>(4);
@@ -317,7 +316,7 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
                         p->gemm_ws_bytes, st);
             return;
         }
-        launch_chol_inv(p->G, k, p->W, p->Linv, p->status, st);  // Linv holds L^{-1}
+        launch_chol_inv(p->G, k, p->W, p->Linv, p->status, p->scratch, st);  // Linv holds L^{-1}
         launch_gemm(false, true, rows, k, k, in, k, p->Linv, k, out, k, nullptr, nullptr, p->gemm_ws,
                     p->gemm_ws_bytes, st);
     };

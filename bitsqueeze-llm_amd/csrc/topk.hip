@@ -625,6 +625,148 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     }
 }
 
+// The composite key of rank `rank` (0 = largest) of one row: MSB-first 8-bit
+// radix select over the 48-bit composite keys (unique per column, so the
+// result is exact).  Uniform across the workgroup.
+template <class F>
+__device__ unsigned long long radix_select48(Shared &sh, uint32_t cols, uint32_t rank, F &&value_at) {
+    unsigned long long prefix = 0, mask = 0;
+    uint32_t remaining = rank + 1;
+    for (int shift = 40; shift >= 0; shift -= 8) {
+        sh.hist[threadIdx.x] = 0;
+        __syncthreads();
+        for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
+            const unsigned long long K = composite_key(value_at(c), c);
+            if ((K & mask) == prefix) atomicAdd(&sh.hist[static_cast<uint32_t>(K >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        choose_digit(sh, remaining);
+        prefix |= static_cast<unsigned long long>(sh.digit) << shift;
+        mask |= 255ull << shift;
+        remaining -= sh.above;
+        __syncthreads();
+    }
+    return prefix;
+}
+
+// Top-k with k above kTopkMaxK (up to every column of the row): workgroup
+// (r, b) emits the ranks [b * kTopkMaxK, min(k, (b + 1) * kTopkMaxK)) of row
+// r.  Its rank boundaries come from two radix selects; the band's entries
+// (at most kTopkMaxK, keys unique) are collected and bitonic-sorted in LDS.
+// The row is cached in LDS when it fits.  Separation, when asked for, is a
+// second pass (topk_separate_kernel) over the emitted indices, since the
+// bands of a row run in different workgroups.
+template <TopkSource SRC, bool CACHED>
+__global__ __launch_bounds__(kThreads) void topk_band_kernel(TopkArgs a) {
+    extern __shared__ unsigned char dyn[];
+    __shared__ Shared sh;
+    const uint32_t cols = a.cols, k = a.k;
+    const uint32_t r = blockIdx.x;
+    const uint32_t lo = blockIdx.y * kTopkMaxK, hi = min(k, lo + kTopkMaxK);
+    const uint64_t row0 = static_cast<uint64_t>(r) * cols;
+    float *cache = reinterpret_cast<float *>(dyn);
+    const uint32_t cache_bytes = CACHED ? ((cols * 4 + 15) & ~15u) : 0u;
+    uint32_t P = 1;
+    while (P < hi - lo) P <<= 1;
+    unsigned long long *cand = reinterpret_cast<unsigned long long *>(dyn + cache_bytes);
+    if (threadIdx.x < 16) {
+        constexpr float Lc[16] = BSQ_NF4_LEVELS;
+        sh.L[threadIdx.x] = Lc[threadIdx.x];
+    }
+    if (threadIdx.x == 0) sh.ncand = 0;
+    float dq = 1.0f;
+    if constexpr (SRC == TopkSource::DenseMinusNF4DQ) {
+        dq = *a.dq;
+        if (dq == 0.0f || !__builtin_isfinite(dq)) dq = 1.0f;
+    }
+    __syncthreads();
+    bool nonzero = false;
+    for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
+        const float v = load_value<SRC>(a, sh.L, dq, row0 + c);
+        if constexpr (CACHED) cache[c] = v;
+        nonzero |= fabsf(v) > FLT_EPSILON;
+    }
+    if (a.flags && blockIdx.y == 0 && __syncthreads_or(nonzero ? 1 : 0)) {
+        if (threadIdx.x == 0) atomicOr(a.flags, kFlagError);
+    }
+    __syncthreads();
+    auto value_at = [&](uint32_t c) -> float {
+        if constexpr (CACHED) return cache[c];
+        else return load_value<SRC>(a, sh.L, dq, row0 + c);
+    };
+    // band: lower <= K (rank hi - 1), and K < upper (rank lo - 1) unless lo == 0
+    const unsigned long long lower = radix_select48(sh, cols, hi - 1, value_at);
+    const unsigned long long upper = lo > 0 ? radix_select48(sh, cols, lo - 1, value_at) : ~0ull;
+    for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
+        const unsigned long long K = composite_key(value_at(c), c);
+        if (K >= lower && (lo == 0 || K < upper)) {
+            const uint32_t slot = atomicAdd(&sh.ncand, 1u);
+            if (slot < P) cand[slot] = K;
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = (hi - lo) + threadIdx.x; i < P; i += kThreads) cand[i] = 0ull;  // pads sort last
+    __syncthreads();
+    for (uint32_t size = 2; size <= P; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = threadIdx.x; i < P / 2; i += kThreads) {
+                const uint32_t l = 2 * i - (i & (stride - 1));
+                const uint32_t h = l + stride;
+                const bool desc = (l & size) == 0;
+                const unsigned long long x = cand[l], y = cand[h];
+                if ((x < y) == desc) {
+                    cand[l] = y;
+                    cand[h] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    uint16_t *out_idx = a.indices + static_cast<uint64_t>(r) * k + lo;
+    float *out_val = a.values + static_cast<uint64_t>(r) * k + lo;
+    for (uint32_t j = threadIdx.x; j < hi - lo; j += kThreads) {
+        const uint32_t col = 0xFFFFu - static_cast<uint32_t>(cand[j] & 0xFFFFu);
+        out_idx[j] = static_cast<uint16_t>(col);
+        out_val[j] = value_at(col);
+    }
+}
+
+// residual = a with the k selected columns of every row zeroed
+// (zero_selected_entries_kernel, topk_cuda_utils.cuh:95-111); the residual
+// may alias the input.  One workgroup per row.
+__global__ __launch_bounds__(kThreads) void topk_separate_kernel(const float *__restrict__ a, float *residual,
+                                                                 uint32_t cols, uint32_t k,
+                                                                 const uint16_t *__restrict__ idx) {
+    const uint64_t row0 = static_cast<uint64_t>(blockIdx.x) * cols;
+    if (residual != a)
+        for (uint32_t c = threadIdx.x; c < cols; c += kThreads) residual[row0 + c] = a[row0 + c];
+    __syncthreads();
+    const uint16_t *ri = idx + static_cast<uint64_t>(blockIdx.x) * k;
+    for (uint32_t j = threadIdx.x; j < k; j += kThreads) residual[row0 + ri[j]] = 0.0f;
+}
+
+template <TopkSource SRC>
+void launch_band(const TopkArgs &a, hipStream_t stream) {
+    const bool cached = a.cols <= kCacheMaxCols;
+    const size_t cache_bytes = cached ? ((a.cols * 4u + 15u) & ~15u) : 0u;
+    const size_t lds = cache_bytes + static_cast<size_t>(kTopkMaxK) * 8;
+    BSQ_REQUIRE(lds + sizeof(Shared) <= 160u * 1024u, "top-k: band does not fit in LDS");
+    const dim3 grid(a.rows, static_cast<unsigned>(ceil_div(a.k, kTopkMaxK)));
+    auto run = [&](auto kern) {
+        BSQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(lds)));
+        kern<<<grid, kThreads, lds, stream>>>(a);
+        BSQ_HIP(hipGetLastError());
+    };
+    if (cached) run(topk_band_kernel<SRC, true>);
+    else run(topk_band_kernel<SRC, false>);
+    if (a.residual) {
+        BSQ_REQUIRE(SRC == TopkSource::Dense, "top-k: separation reads a dense source");
+        topk_separate_kernel<<<a.rows, kThreads, 0, stream>>>(a.a, a.residual, a.cols, a.k, a.indices);
+        BSQ_HIP(hipGetLastError());
+    }
+}
+
 template <TopkSource SRC, int NV4>
 void launch_reg(const TopkArgs &a, hipStream_t stream) {
     topk_reg_kernel<SRC, NV4><<<a.rows, kThreads, 0, stream>>>(a);
@@ -696,6 +838,10 @@ __global__ __launch_bounds__(256) void topk_scatter_flat_kernel(const uint16_t *
 
 template <TopkSource SRC>
 void launch_src(const TopkArgs &a, hipStream_t stream) {
+    if (a.k > kTopkMaxK) {
+        launch_band<SRC>(a, stream);
+        return;
+    }
     if (try_launch_reg<SRC>(a, stream)) return;
     uint32_t P = 1;
     while (P < a.k) P <<= 1;
@@ -724,7 +870,6 @@ void launch_src(const TopkArgs &a, hipStream_t stream) {
 void launch_topk_select(const TopkArgs &a, hipStream_t stream) {
     BSQ_REQUIRE(a.rows > 0 && a.cols > 0 && a.cols <= 65535 && a.rows <= 65535, "top-k: bad shape");
     BSQ_REQUIRE(a.k >= 1 && a.k <= a.cols, "top-k: k must be in [1, cols]");
-    BSQ_REQUIRE(a.k <= kTopkMaxK, "top-k: k above the supported maximum (8192)");
     BSQ_REQUIRE(a.a && a.indices && a.values, "top-k: null pointer");
     switch (a.source) {
         case TopkSource::Dense: launch_src<TopkSource::Dense>(a, stream); break;
