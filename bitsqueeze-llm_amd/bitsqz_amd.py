@@ -112,6 +112,7 @@ def lib():
         "bsq_quant_nf4_code_sweep": (i32, [u64, u64, P, P, P]),
         "bsq_nf4_thresholds": (None, [P]),
         "bsq_svd_lowrank": (i32, [P, i32, i32, i32, i32, P, u64, P, P, P, P]),
+        "bsq_svd_lowrank_noalloc": (i32, [P, i32, i32, i32, i32, P, u64, P, P, P, P]),
         "bsq_reconstruct_lowrank": (i32, [P, P, P, i32, i32, i32, P, P]),
         "bsq_gaussian_fill": (i32, [P, u64, u64, P]),
         "bsq_device_count": (i32, [C.POINTER(i32)]),

@@ -146,6 +146,14 @@ struct SvdPlan;
 SvdPlan *svd_plan_create(int m, int n, int q, int niter);
 void svd_plan_destroy(SvdPlan *plan) noexcept;
 int svd_plan_rank(const SvdPlan *plan);
+// Device bytes of every buffer of such a plan, each rounded up to 256 bytes.
+uint64_t svd_plan_arena_bytes(int m, int n, int q, int niter);
+// svd_run on a plan carved from the library's fixed device scratch array (no
+// device allocation; asynchronous on `stream`; fails for shapes whose plan
+// exceeds svd_noalloc_scratch_bytes()).
+void svd_run_noalloc(const float *A, int m, int n, int q, int niter, const float *sketch, uint64_t seed, float *U,
+                     float *S, float *V, hipStream_t stream);
+uint64_t svd_noalloc_scratch_bytes();
 // U (m x q), S (q), V (n x q), all row-major.  `sketch` (min(m,n) x q,
 // row-major, device) replaces the built-in Gaussian sketch when not null.
 void svd_run(SvdPlan *plan, const float *A, const float *sketch, uint64_t seed, float *U, float *S, float *V,

@@ -1226,6 +1226,13 @@ int bsq_svd_lowrank(const float *d_A, int m, int n, int q, int niter, const floa
     });
 }
 
+int bsq_svd_lowrank_noalloc(const float *d_A, int m, int n, int q, int niter, const float *d_sketch, uint64_t seed,
+                            float *d_U, float *d_S, float *d_V, void *stream) {
+    return guarded([&] {
+        svd_run_noalloc(d_A, m, n, q, niter, d_sketch, seed, d_U, d_S, d_V, static_cast<hipStream_t>(stream));
+    });
+}
+
 int bsq_reconstruct_lowrank(const float *d_U, const float *d_S, const float *d_V, int m, int n, int k, float *d_out,
                             void *stream) {
     return guarded([&] {

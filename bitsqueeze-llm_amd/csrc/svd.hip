@@ -18,6 +18,9 @@
 #include "bsq_internal.hpp"
 
 #include <algorithm>
+#include <mutex>
+#include <string>
+#include <type_traits>
 
 namespace bsq {
 
@@ -205,8 +208,10 @@ struct SvdPlan {
     double *gram_ws = nullptr;
     float *gemm_ws = nullptr;
     uint64_t gemm_ws_bytes = 0;
+    bool owns = true;  // buffers from hipMalloc (freed here), else carved from a caller's arena
 
     ~SvdPlan() {
+        if (!owns) return;
         release(R);
         release(X);
         release(X2);
@@ -233,51 +238,100 @@ struct SvdPlan {
     }
 };
 
-SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
+namespace {
+
+// Shape fields of a plan (k = max(1, min(q, m, n)), svd_lowrank_cuda.cu:129-137).
+void plan_shape(SvdPlan &p, int m, int n, int q, int niter) {
     BSQ_REQUIRE(m > 0 && n > 0 && q > 0 && niter >= 0, "svd: bad arguments");
+    p.m = m;
+    p.n = n;
+    p.k = std::max(1, std::min(q, std::min(m, n)));
+    p.niter = niter;
+    p.transposed = m < n;
+    p.Mw = p.transposed ? n : m;
+    p.Nw = p.transposed ? m : n;
+}
+
+// Every device buffer of the plan, in one place: `get(ptr, count)` sets each
+// pointer (hipMalloc per buffer, or a bump pointer over an arena).
+template <class Get>
+void plan_buffers(SvdPlan &p, Get &&get) {
+    const uint64_t k = p.k;
+    get(p.R, p.Nw * k);
+    get(p.X, p.Mw * k);
+    get(p.X2, p.Mw * k);
+    get(p.Y, p.Nw * k);
+    get(p.Y2, p.Nw * k);
+    get(p.Linv, k * k);
+    get(p.Uh, k * k);
+    get(p.G, k * k);
+    get(p.W, k * k);
+    if (chol_blocked_supported(static_cast<int>(k))) get(p.Lbuf, chol_blocked_buffer_doubles(static_cast<int>(k)));
+    get(p.Z, k * k);
+    get(p.small, 4 * k + 8);
+    get(p.cbest, kColChunks * k);
+    get(p.cidx, kColChunks * k);
+    get(p.csum, kColChunks * k);
+    get(p.rowsq, k);
+    get(p.csign, 2 * k);
+    get(p.scratch, 9 * k * k + 2 * k);
+    get(p.lambda, k);
+    get(p.iscratch, 2 * k * k);
+    get(p.status, 4);
+    const uint64_t gw = std::max(gram_workspace_bytes(p.Mw, p.k), gram_workspace_bytes(p.Nw, p.k));
+    get(p.gram_ws, gw / sizeof(double) + 1);
+    uint64_t ws = 0;
+    ws = std::max(ws, gemm_workspace_bytes(p.Mw, p.k, p.Nw));
+    ws = std::max(ws, gemm_workspace_bytes(p.Nw, p.k, p.Mw));
+    p.gemm_ws_bytes = ws;
+    if (ws) get(p.gemm_ws, ws / sizeof(float));
+}
+
+constexpr uint64_t kArenaAlign = 256;
+
+}  // namespace
+
+SvdPlan *svd_plan_create(int m, int n, int q, int niter) {
     auto *p = new SvdPlan;
     try {
-        p->m = m;
-        p->n = n;
-        p->k = std::max(1, std::min(q, std::min(m, n)));
-        p->niter = niter;
-        p->transposed = m < n;
-        p->Mw = p->transposed ? n : m;
-        p->Nw = p->transposed ? m : n;
-        const uint64_t k = p->k;
-        p->R = alloc<float>(p->Nw * k);
-        p->X = alloc<float>(p->Mw * k);
-        p->X2 = alloc<float>(p->Mw * k);
-        p->Y = alloc<float>(p->Nw * k);
-        p->Y2 = alloc<float>(p->Nw * k);
-        p->Linv = alloc<float>(k * k);
-        p->Uh = alloc<float>(k * k);
-        p->G = alloc<double>(k * k);
-        p->W = alloc<double>(k * k);
-        if (chol_blocked_supported(static_cast<int>(k))) p->Lbuf = alloc<double>(chol_blocked_buffer_doubles(static_cast<int>(k)));
-        p->Z = alloc<double>(k * k);
-        p->small = alloc<double>(4 * k + 8);
-        p->cbest = alloc<float>(kColChunks * k);
-        p->cidx = alloc<int>(kColChunks * k);
-        p->csum = alloc<double>(kColChunks * k);
-        p->rowsq = alloc<double>(k);
-        p->csign = alloc<float>(2 * k);
-        p->scratch = alloc<double>(9 * k * k + 2 * k);
-        p->lambda = alloc<double>(k);
-        p->iscratch = alloc<int>(2 * k * k);
-        p->status = alloc<int>(4);
-        const uint64_t gw = std::max(gram_workspace_bytes(p->Mw, p->k), gram_workspace_bytes(p->Nw, p->k));
-        p->gram_ws = alloc<double>(gw / sizeof(double) + 1);
-        uint64_t ws = 0;
-        ws = std::max(ws, gemm_workspace_bytes(p->Mw, p->k, p->Nw));
-        ws = std::max(ws, gemm_workspace_bytes(p->Nw, p->k, p->Mw));
-        p->gemm_ws_bytes = ws;
-        p->gemm_ws = ws ? alloc<float>(ws / sizeof(float)) : nullptr;
+        plan_shape(*p, m, n, q, niter);
+        plan_buffers(*p, [](auto *&ptr, uint64_t count) {
+            using T = std::remove_reference_t<decltype(*ptr)>;
+            ptr = alloc<T>(count);
+        });
     } catch (...) {
         delete p;
         throw;
     }
     return p;
+}
+
+uint64_t svd_plan_arena_bytes(int m, int n, int q, int niter) {
+    SvdPlan p;
+    p.owns = false;
+    plan_shape(p, m, n, q, niter);
+    uint64_t total = 0;
+    plan_buffers(p, [&](auto *&ptr, uint64_t count) {
+        using T = std::remove_reference_t<decltype(*ptr)>;
+        total += ceil_div(count * sizeof(T), kArenaAlign) * kArenaAlign;
+        ptr = nullptr;
+    });
+    return total;
+}
+
+void svd_plan_init_arena(SvdPlan &p, int m, int n, int q, int niter, void *arena, uint64_t arena_bytes) {
+    BSQ_REQUIRE(arena && (reinterpret_cast<uintptr_t>(arena) % kArenaAlign) == 0, "svd: arena not 256-byte aligned");
+    p.owns = false;
+    plan_shape(p, m, n, q, niter);
+    const uint64_t need = svd_plan_arena_bytes(m, n, q, niter);
+    BSQ_REQUIRE(need <= arena_bytes, "svd: shape needs more scratch than the arena holds");
+    auto *base = static_cast<uint8_t *>(arena);
+    uint64_t off = 0;
+    plan_buffers(p, [&](auto *&ptr, uint64_t count) {
+        using T = std::remove_reference_t<decltype(*ptr)>;
+        ptr = reinterpret_cast<T *>(base + off);
+        off += ceil_div(count * sizeof(T), kArenaAlign) * kArenaAlign;
+    });
 }
 
 void svd_plan_destroy(SvdPlan *plan) noexcept { delete plan; }
@@ -392,5 +446,58 @@ void launch_gaussian_fill(float *out, uint64_t n, uint64_t seed, hipStream_t str
     gaussian_fill_kernel<<<static_cast<unsigned>(grid), 256, 0, stream>>>(out, n, seed);
     BSQ_HIP(hipGetLastError());
 }
+
+// ---------------------------------------------------------------------------
+// No-allocation variant of the standalone SVD (bsq_svd_lowrank_noalloc): the
+// plan's buffers are carved out of one file-scope device array instead of
+// hipMalloc'ed per call, for callers that cannot allocate (code under HIP
+// graph capture, allocation-free serving loops).  Every call on a GPU uses
+// that GPU's copy of the array, so calls that overlap on one GPU race.  The
+// SVD kernels write every scratch word before reading it (nothing needs to
+// start at zero), so the contents a previous call left behind do not matter.
+// ---------------------------------------------------------------------------
+constexpr uint64_t kNoAllocScratchBytes = 256ull << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (each GPU holds its own copy at its own
+// address; the host-side name is not a device address).
+void *scratch_address() {
+    int dev = 0;
+    BSQ_HIP(hipGetDevice(&dev));
+    BSQ_REQUIRE(dev >= 0 && dev < kMaxDevices, "svd noalloc: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        BSQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        BSQ_REQUIRE(p != nullptr, "svd noalloc: scratch symbol has no device address");
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+void svd_run_noalloc(const float *A, int m, int n, int q, int niter, const float *sketch, uint64_t seed, float *U,
+                     float *S, float *V, hipStream_t stream) {
+    BSQ_REQUIRE(A && U && S && V, "svd noalloc: null argument");
+    BSQ_REQUIRE(m > 0 && n > 0 && q > 0 && niter >= 0, "svd noalloc: bad shape");
+    const uint64_t need = svd_plan_arena_bytes(m, n, q, niter);
+    if (need > kNoAllocScratchBytes)
+        fail("svd noalloc: this shape needs " + std::to_string(need) + " bytes of scratch, above the " +
+             std::to_string(kNoAllocScratchBytes) + " bytes the no-allocation entry point holds");
+    void *arena = scratch_address();
+    SvdPlan plan;
+    svd_plan_init_arena(plan, m, n, q, niter, arena, kNoAllocScratchBytes);
+    svd_run(&plan, A, sketch, seed, U, S, V, stream);
+}
+
+uint64_t svd_noalloc_scratch_bytes() { return kNoAllocScratchBytes; }
 
 }  // namespace bsq

@@ -201,6 +201,19 @@ BSQ_API int bsq_svd_lowrank(const float *d_A, int m, int n, int q, int niter,
                             const float *d_sketch, uint64_t seed, float *d_U, float *d_S,
                             float *d_V, void *stream);
 
+/* bsq_svd_lowrank without any device allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, allocation-free serving loops).  Same arguments and results
+ * as bsq_svd_lowrank (the same kernels on the same plan layout), but the
+ * plan's buffers are carved from the library's fixed 256 MiB device array
+ * (one copy per GPU, held until the process ends), so shapes whose plan needs
+ * more return 1 with the byte counts in bsq_last_error().  Asynchronous on
+ * `stream` (no synchronisation); calls that overlap on one GPU share that
+ * array and race. */
+BSQ_API int bsq_svd_lowrank_noalloc(const float *d_A, int m, int n, int q, int niter,
+                                    const float *d_sketch, uint64_t seed, float *d_U,
+                                    float *d_S, float *d_V, void *stream);
+
 /* out (m x n, row-major) = U (m x k) * diag(S) * V (n x k)^T.
  * replaces reconstruct_lowrank_cuda, reference
  * modules/reconstruct_lowrank_cuda/src/reconstruct_lowrank_cuda.cu:21-62,153-171. */
