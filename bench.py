@@ -160,20 +160,39 @@ def roofline_time_ms(rows, cols, svd, nit, q, err_on, payload_bytes):
     return (8.0 * n + 2.0 * payload_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
 
 
-def cpu_baseline(x, direct, budget_s=12.0):
-    """The reference's legacy OpenMP NF4 / NF4_DQ codec (compiled from the
-    reference's own sources into oracle/_ref) on a bounded row sample of the
-    same matrix; falls back to the repository's C restatement (kind 'port')
-    when that library is absent."""
+def host_cpu_info():
+    """nproc, CPU model and socket count of this host (/proc/cpuinfo)."""
+    model, sockets = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("physical id"):
+                sockets.add(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return os.cpu_count() or 1, model, max(1, len(sockets))
+
+
+def cpu_baseline(x, direct, reps=5):
+    """The reference's legacy OpenMP NF4 / NF4_DQ codec (nf4_impl.cpp:92-164,
+    nf4_dq_impl.cpp:162-275, compiled from the reference's own sources into
+    oracle/_ref) on the same matrix: compress and decompress timed
+    separately, one warmup then the median of `reps`, with every host thread
+    this job may use (OMP_NUM_THREADS, else nproc) and with one thread.  The
+    thread count is set inside the library (omp_set_num_threads) and read
+    back, so `cores` is what ran.  Falls back to the repository's C
+    restatement (kind 'port') when that library is absent.  The reference
+    has no CPU top-k, SVD or reconstruct."""
     import ctypes
 
     from oracle import oracle as O
 
     method = direct if direct != B.QUANT_NONE else B.NF4
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    nproc, model, sockets = host_cpu_info()
+    want = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc
     ref_so = os.path.join(ROOT, "oracle", "_ref", "libref_nf4.so")
-    rows = x.shape[0]  # the whole matrix, repeated for about budget_s seconds
-    sample = np.ascontiguousarray(x[:rows])
+    sample = np.ascontiguousarray(x, np.float32)
     n = sample.size
     nb, nc = (n + 63) // 64, (n + 1) // 2
     out = np.empty(n, np.float32)
@@ -182,13 +201,18 @@ def cpu_baseline(x, direct, budget_s=12.0):
     if os.path.exists(ref_so):
         L = ctypes.CDLL(ref_so)
         kind = "reference"
+        L.ref_set_threads.argtypes = [ctypes.c_int]
+        L.ref_set_threads.restype = ctypes.c_int
+        set_threads = L.ref_set_threads
         if method == B.NF4:
             L.ref_nf4_compress.argtypes = [P, ctypes.c_ulonglong, P, P]
             L.ref_nf4_decompress.argtypes = [P, P, ctypes.c_ulonglong, P]
             sc = np.empty(nb, np.float32)
 
-            def once():
+            def comp():
                 L.ref_nf4_compress(sample.ctypes.data, n, sc.ctypes.data, codes.ctypes.data)
+
+            def decomp():
                 L.ref_nf4_decompress(sc.ctypes.data, codes.ctypes.data, n, out.ctypes.data)
         else:
             L.ref_nf4dq_compress.argtypes = [P, ctypes.c_ulonglong, P, P, P]
@@ -196,30 +220,49 @@ def cpu_baseline(x, direct, budget_s=12.0):
             sc = np.empty(nb, np.uint8)
             dq = np.zeros(1, np.float32)
 
-            def once():
+            def comp():
                 L.ref_nf4dq_compress(sample.ctypes.data, n, dq.ctypes.data, sc.ctypes.data, codes.ctypes.data)
+
+            def decomp():
                 L.ref_nf4dq_decompress(ctypes.c_float(dq[0]), sc.ctypes.data, codes.ctypes.data, n,
                                        out.ctypes.data)
     else:
         kind = "port"
+        holder = {}
+        set_threads = None
 
-        def once():
-            q = O.quant_compress(sample, method)
-            O.quant_decompress(q)
-    once()
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        once()
-        reps += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    gbs = 4 * n / dt / 1e9
+        def comp():
+            holder["q"] = O.quant_compress(sample, method)
+
+        def decomp():
+            O.quant_decompress(holder["q"])
+
+    def median_ms(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append((time.perf_counter() - t0) * 1e3)
+        return float(np.median(ts))
+
+    runs = {}
+    for label, t in (("all", want), ("one", 1)):
+        used = set_threads(t) if set_threads else int(os.environ.get("OMP_NUM_THREADS", "0") or nproc)
+        cm = median_ms(comp)
+        dm = median_ms(decomp)
+        runs[label] = {"threads": used, "compress_ms": round(cm, 3), "decompress_ms": round(dm, 3),
+                       "gbps_fp32_in": round(4 * n / ((cm + dm) * 1e-3) / 1e9, 3)}
+    if set_threads:
+        set_threads(want)
     label = "NF4" if method == B.NF4 else "NF4_DQ"
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"legacy {label} compress+decompress of the full {rows}x{x.shape[1]} matrix, "
-                      f"{reps} reps in {reps * dt:.1f} s; the reference has no CPU top-k / SVD path"}
+    a = runs["all"]
+    return {"value": a["gbps_fp32_in"], "unit": "GB/s", "cores": a["threads"], "kind": kind,
+            "sample": f"legacy {label} compress and decompress of the full {x.shape[0]}x{x.shape[1]} matrix "
+                      f"({4 * n} bytes in), 1 warmup + median of {reps} each; the reference has no CPU "
+                      f"top-k / SVD path",
+            "compress_ms": a["compress_ms"], "decompress_ms": a["decompress_ms"],
+            "one_thread": runs["one"], "nproc": nproc, "cpu_model": model, "sockets": sockets}
 
 
 def main():

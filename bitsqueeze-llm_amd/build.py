@@ -1,6 +1,7 @@
 """Builds the MI355X (gfx950) bitsqz_llm library in-tree.
 
     python bitsqueeze-llm_amd/build.py        # -> bitsqueeze-llm_amd/lib/libbitsqz_llm_lib.so
+    python bitsqueeze-llm_amd/build.py --package   # + the installed CMake package under _install/
 
 Every HIP source under csrc/ is compiled with hipcc for gfx950 into an object
 under _build/, and the objects are linked into one shared library whose
@@ -61,6 +62,41 @@ def _compile(src: str) -> str:
     return obj
 
 
+INSTALL = os.path.join(HERE, "_install")
+CMAKE_BUILD = os.path.join(BUILD, "cmake")
+CONSUMER_SRC = os.path.join(ROOT, "tests", "cmake_consumer")
+CONSUMER_BUILD = os.path.join(CONSUMER_SRC, "_build")
+CONSUMER_BIN = os.path.join(CONSUMER_BUILD, "bsq_consumer")
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"failed: {' '.join(cmd)}\n{r.stdout[-4000:]}\n{r.stderr[-4000:]}")
+
+
+def package(verbose: bool = True) -> str:
+    """The installed CMake package (CMakeLists.txt beside this file): builds
+    the same sources into libbitsqz_llm_lib.so.0.1.0 and installs it, the
+    headers and bitsqz_llmConfig.cmake under _install/; then builds the
+    downstream test program tests/cmake_consumer against that installed
+    package with find_package(bitsqz_llm CONFIG)."""
+    cmake = shutil.which("cmake")
+    if not cmake:
+        raise RuntimeError("cmake not found")
+    jobs = str(max(1, min(8, os.cpu_count() or 1)))
+    _run([cmake, "-S", HERE, "-B", CMAKE_BUILD, f"-DCMAKE_INSTALL_PREFIX={INSTALL}", "-DCMAKE_BUILD_TYPE=Release",
+          f"-DCMAKE_HIP_ARCHITECTURES={ARCH}"])
+    _run([cmake, "--build", CMAKE_BUILD, "-j", jobs])
+    _run([cmake, "--install", CMAKE_BUILD])
+    _run([cmake, "-S", CONSUMER_SRC, "-B", CONSUMER_BUILD, f"-DCMAKE_PREFIX_PATH={INSTALL}",
+          "-DCMAKE_BUILD_TYPE=Release"])
+    _run([cmake, "--build", CONSUMER_BUILD, "-j", jobs])
+    if verbose:
+        print(f"installed the CMake package under {INSTALL}; built {CONSUMER_BIN}")
+    return INSTALL
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
@@ -83,6 +119,8 @@ def build(verbose: bool = True) -> str:
 if __name__ == "__main__":
     try:
         build()
+        if "--package" in sys.argv:
+            package()
     except RuntimeError as e:
         print(e, file=sys.stderr)
         sys.exit(1)

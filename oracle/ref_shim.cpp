@@ -7,9 +7,19 @@
 #include <quantization/impl/nf4_dq_impl.hpp>
 #include <quantization/impl/nf4_impl.hpp>
 
+#include <omp.h>
+
 #include <cstring>
 
 extern "C" {
+
+// Sets the OpenMP thread count the reference codec's parallel loops use
+// (nf4_impl.cpp:104, nf4_dq_impl.cpp:174,197,255) and returns the count in
+// effect, so a timing reports the threads that actually ran.
+__attribute__((visibility("default"))) int ref_set_threads(int n) {
+    if (n > 0) omp_set_num_threads(n);
+    return omp_get_max_threads();
+}
 
 // Runs nf4_compress (nf4_impl.cpp:92-135) and copies the block scales and
 // codes out of the reference's own allocation.

@@ -254,3 +254,44 @@ def test_load_rejects_wrapped_payload_end():
     assert not O.load_accepts(buf)
     cb = C.create_string_buffer(buf, len(buf))
     assert not B.lib().bsq_load_from_buffer(cb, len(buf))
+
+
+# ------------------------------------------------------- installed package --
+INSTALL = os.path.join(ROOT, "bitsqueeze-llm_amd", "_install")
+CONSUMER = os.path.join(ROOT, "tests", "cmake_consumer", "_build", "bsq_consumer")
+
+
+def test_installed_cmake_package_layout():
+    """The package the reference's downstream users consume
+    (CMakeLists.txt:60-124, cmake/bitsqz_llmConfig.cmake.in:1-13): the
+    versioned library with the reference's SONAME, both headers, and a config
+    exporting bitsqz_llm::bitsqz_llm with hip::host as a public dependency."""
+    lib = os.path.join(INSTALL, "lib")
+    cm = os.path.join(lib, "cmake", "bitsqz_llm")
+    for f in ("libbitsqz_llm_lib.so.0.1.0", "libbitsqz_llm_lib.so.0", "libbitsqz_llm_lib.so"):
+        assert os.path.exists(os.path.join(lib, f)), f
+    assert os.path.realpath(os.path.join(lib, "libbitsqz_llm_lib.so")).endswith("libbitsqz_llm_lib.so.0.1.0")
+    for f in ("bitsqz_llm.hpp", "bitsqz_llm_c.h"):
+        assert os.path.exists(os.path.join(INSTALL, "include", f)), f
+    cfg = open(os.path.join(cm, "bitsqz_llmConfig.cmake")).read()
+    assert "find_dependency(hip" in cfg
+    targets = open(os.path.join(cm, "bitsqz_llmTargets.cmake")).read()
+    assert "bitsqz_llm::bitsqz_llm" in targets and "hip::host" in targets
+    assert 'PACKAGE_VERSION "0.1.0"' in open(os.path.join(cm, "bitsqz_llmConfigVersion.cmake")).read()
+    out = subprocess.run(["readelf", "-d", os.path.join(lib, "libbitsqz_llm_lib.so.0.1.0")], capture_output=True,
+                         text=True, check=True).stdout
+    assert "[libbitsqz_llm_lib.so.0]" in out
+    syms = subprocess.run(["nm", "-D", "--defined-only", os.path.join(lib, "libbitsqz_llm_lib.so.0.1.0")],
+                          capture_output=True, text=True, check=True).stdout
+    assert all(m in syms for m in MANGLED)
+
+
+def test_consumer_links_the_nine_mangled_functions():
+    """The downstream program (tests/cmake_consumer, built through
+    find_package against the installed package) binds all nine C++-linkage
+    functions by their reference mangling and loads the installed library."""
+    undef = subprocess.run(["nm", "--undefined-only", CONSUMER], capture_output=True, text=True,
+                           check=True).stdout
+    assert all(m in undef for m in MANGLED[:9])
+    dyn = subprocess.run(["readelf", "-d", CONSUMER], capture_output=True, text=True, check=True).stdout
+    assert "libbitsqz_llm_lib.so.0" in dyn and os.path.join(INSTALL, "lib") in dyn
