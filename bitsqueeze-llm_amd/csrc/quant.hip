@@ -7,10 +7,11 @@
 //   reference's own test requires to equal the CUDA codec exactly,
 //   tests/quantization_cuda/test_nf4_cuda.cu:109-114).
 //
-// Layout of the work: one thread owns 8 consecutive elements (two 16-byte
-// loads, one 4-byte store of packed nibbles), so one 64-element block is an
-// aligned group of 8 lanes and its absmax is a 3-step DPP reduction.  Kernels
-// are persistent grid-stride loops sized to the CU count.
+// Layout of the work: the encoders give a lane 8 consecutive elements (a
+// 64-element block is an aligned group of 8 lanes, its absmax a 3-step DPP
+// reduction); the decoder stages 4096-element tiles through LDS so that its
+// stores are contiguous per instruction.  Kernels are persistent grid-stride
+// loops sized to the CU count.
 //
 // This file is compiled with -ffp-contract=off: every multiply and subtract
 // below must round on its own, as in the reference.
@@ -43,15 +44,42 @@ __device__ __noinline__ uint32_t nf4_code_scan(float v) {
     return best;
 }
 
-// Nearest NF4 code with the reference's tie rule.  For |v| < 2 the scan's
-// answer is the number of exact decision thresholds at or below v.
-__device__ __forceinline__ uint32_t nf4_code(float v) {
+// Nearest NF4 code with the reference's tie rule: for |v| < 2 the scan's
+// answer is the number of exact decision thresholds at or below v, found
+// here with one table lookup and one comparison.  [-1, 1] is
+// cut into 256 bins of width 1/128; bin b holds code_lo = #{T_i <= -1 + b/128}
+// and the threshold lying inside the bin, if any (no bin holds two: the
+// closest thresholds are 0.085 apart).  Every threshold is at least 2.3e-4
+// from a bin edge, while the bin index floor((v + 1) * 128) computed in FP32
+// is off by one only for v within 1.2e-7 of an edge, where the count is the
+// same on both sides; v in [1, 2) and (-2, -1] clamp to the end bins (codes
+// 15 and 0).  |v| >= 2 and non-finite v take the scan.  Exhaustively
+// checked against the scan over all 2^32 floats by the GPU test suite.
+struct Nf4Table {
+    float thr[256];
+    uint32_t lo[256];
+};
+
+__device__ __forceinline__ void nf4_table_build(Nf4Table &t) {
     constexpr float T[15] = BSQ_NF4_THRESHOLDS;
-    if (fabsf(v) < 2.0f) {
-        uint32_t c = 0;
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+        const float e0 = -1.0f + static_cast<float>(b) / 128.0f, e1 = -1.0f + static_cast<float>(b + 1) / 128.0f;
+        uint32_t lo = 0;
+        float thr = __builtin_inff();
 #pragma unroll
-        for (int i = 0; i < 15; ++i) c += (v >= T[i]) ? 1u : 0u;
-        return c;
+        for (int i = 0; i < 15; ++i) {
+            lo += (T[i] <= e0) ? 1u : 0u;
+            if (T[i] > e0 && T[i] < e1) thr = T[i];
+        }
+        t.thr[b] = thr;
+        t.lo[b] = lo;
+    }
+}
+
+__device__ __forceinline__ uint32_t nf4_code(const Nf4Table &t, float v) {
+    if (fabsf(v) < 2.0f) {
+        const int b = min(max(static_cast<int>((v + 1.0f) * 128.0f), 0), 255);
+        return t.lo[b] + ((v >= t.thr[b]) ? 1u : 0u);
     }
     return nf4_code_scan(v);
 }
@@ -147,6 +175,14 @@ __device__ __forceinline__ float dq_effective(float dq) {
     return (dq == 0.0f || !__builtin_isfinite(dq)) ? 1.0f : dq;
 }
 
+// Encode side: one thread owns chunks of 8 consecutive elements (two 16-byte
+// loads, one 4-byte store of packed nibbles), so a 64-element block is an
+// aligned group of 8 lanes and the per-block scale work is shared by 8 lanes.
+// Each thread takes kUnroll chunks per loop iteration, their loads issued
+// together before any is used (one chunk per iteration left these kernels
+// latency-bound).
+constexpr int kUnroll = 4;
+
 // Pass 1 of NF4_DQ: max over blocks of the block scale (absmax, or 1 for an
 // all-zero block), accumulated as float bits (all values >= 0) with one
 // atomicMax per workgroup.  Replaces compute_block_absmax_kernel +
@@ -154,20 +190,27 @@ __device__ __forceinline__ float dq_effective(float dq) {
 __global__ __launch_bounds__(kThreads) void dq_gmax_kernel(const float *__restrict__ x, uint64_t n,
                                                             bool vec_ok, uint32_t *__restrict__ gmax) {
     const uint64_t nchunks = ceil_div(n, 8), nblocks = ceil_div(n, kQuantBlock);
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
     float local = 0.0f;
-    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads; base < nchunks;
-         base += static_cast<uint64_t>(gridDim.x) * kThreads) {
-        const uint64_t chunk = base + threadIdx.x;
-        float v[8];
-        if (chunk < nchunks) load8(x, n, chunk, vec_ok, v);
-        else
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads; base < nchunks; base += kUnroll * stride) {
+        float v[kUnroll][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-        float m = 0.0f;
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t chunk = base + u * stride + threadIdx.x;
+            if (chunk < nchunks) load8(x, n, chunk, vec_ok, v[u]);
+            else
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(sanitize(v[i])));
-        m = group8_max(m);
-        if (chunk / 8 < nblocks) local = fmaxf(local, m > 0.0f ? m : 1.0f);
+                for (int i = 0; i < 8; ++i) v[u][i] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t chunk = base + u * stride + threadIdx.x;
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(sanitize(v[u][i])));
+            m = group8_max(m);
+            if (chunk / 8 < nblocks) local = fmaxf(local, m > 0.0f ? m : 1.0f);
+        }
     }
     // workgroup max
     for (int off = 32; off >= 1; off >>= 1) local = fmaxf(local, __shfl_xor(local, off));
@@ -186,52 +229,72 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     const float *__restrict__ x, uint64_t n, bool vec_ok, float *__restrict__ scales_f32,
     uint8_t *__restrict__ scales_u8, const uint32_t *__restrict__ gmax, float *__restrict__ dq_out,
     uint8_t *__restrict__ codes) {
+    __shared__ Nf4Table tab;
+    nf4_table_build(tab);
     const uint64_t nchunks = ceil_div(n, 8);
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
     float dq = 1.0f;
     if constexpr (DQ) {
         const float raw = dq_raw_from_gmax(*gmax);
         dq = dq_effective(raw);
         if (blockIdx.x == 0 && threadIdx.x == 0) *dq_out = raw;
     }
-    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads; base < nchunks;
-         base += static_cast<uint64_t>(gridDim.x) * kThreads) {
-        const uint64_t chunk = base + threadIdx.x;
-        const bool valid = chunk < nchunks;
-        float v[8];
-        if (valid) load8(x, n, chunk, vec_ok, v);
-        else
+    __syncthreads();
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads; base < nchunks; base += kUnroll * stride) {
+        float v[kUnroll][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t chunk = base + u * stride + threadIdx.x;
+            if (chunk < nchunks) load8(x, n, chunk, vec_ok, v[u]);
+            else
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = sanitize(v[i]);
-        float m = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
-        m = group8_max(m);
-        const float absmax = (m > 0.0f) ? m : 1.0f;
-        float scale;
-        uint32_t scode = 0;
-        if constexpr (DQ) {
-            scode = e4m3_encode(absmax / dq);
-            scale = dq * e4m3_decode(scode);
-            if (scale == 0.0f || !__builtin_isfinite(scale)) scale = 1.0f;
-        } else {
-            scale = absmax;
+                for (int i = 0; i < 8; ++i) v[u][i] = 0.0f;
         }
-        const float inv = 1.0f / scale;
-        if (valid && (threadIdx.x & 7) == 0) {
-            if constexpr (DQ) scales_u8[chunk / 8] = static_cast<uint8_t>(scode);
-            else scales_f32[chunk / 8] = scale;
-        }
-        if (valid) {
-            uint32_t c[8];
-            const uint64_t e0 = chunk * 8;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code(v[i] * inv) : 0u;  // odd tail: low nibble 0
-            store_codes(codes, n, chunk, vec_ok, c);
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t chunk = base + u * stride + threadIdx.x;
+            const bool valid = chunk < nchunks;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[u][i] = sanitize(v[u][i]);
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[u][i]));
+            m = group8_max(m);
+            const float absmax = (m > 0.0f) ? m : 1.0f;
+            float scale;
+            uint32_t scode = 0;
+            if constexpr (DQ) {
+                scode = e4m3_encode(absmax / dq);
+                scale = dq * e4m3_decode(scode);
+                if (scale == 0.0f || !__builtin_isfinite(scale)) scale = 1.0f;
+            } else {
+                scale = absmax;
+            }
+            const float inv = 1.0f / scale;
+            if (valid && (threadIdx.x & 7) == 0) {
+                if constexpr (DQ) scales_u8[chunk / 8] = static_cast<uint8_t>(scode);
+                else scales_f32[chunk / 8] = scale;
+            }
+            if (valid) {
+                uint32_t c[8];
+                const uint64_t e0 = chunk * 8;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code(tab, v[u][i] * inv) : 0u;  // odd tail: low nibble 0
+                store_codes(codes, n, chunk, vec_ok, c);
+            }
         }
     }
 }
+
+// Decode: a workgroup decodes tiles of 4096 elements.  Lane t reads the
+// 8 code bytes and the block scale of elements 16 t .. 16 t + 15 of the tile
+// (one 8-byte load; the 16 elements lie in one 64-element block), writes the
+// 16 values to an LDS tile, and the tile leaves as 16-byte stores in which
+// consecutive lanes write consecutive addresses (each store instruction of
+// the workgroup covers 4 KB contiguously).  Two LDS tiles alternate, so one
+// barrier per tile suffices.  The ragged end of the section (n not a
+// multiple of 4096) is decoded element by element.
+constexpr int kDecTile = kThreads * 16;
 
 template <bool DQ>
 __global__ __launch_bounds__(kThreads) void quant_decode_kernel(
@@ -239,51 +302,59 @@ __global__ __launch_bounds__(kThreads) void quant_decode_kernel(
     const float *__restrict__ dq_ptr, const uint8_t *__restrict__ codes, float *__restrict__ out) {
     constexpr float Lc[16] = BSQ_NF4_LEVELS;
     __shared__ float L[16];
+    __shared__ __attribute__((aligned(16))) float tile[2][kDecTile];
     if (threadIdx.x < 16) L[threadIdx.x] = Lc[threadIdx.x];
     __syncthreads();
-    const uint64_t nchunks = ceil_div(n, 8);
     float dq = 1.0f;
     if constexpr (DQ) dq = dq_effective(*dq_ptr);
-    for (uint64_t chunk = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; chunk < nchunks;
-         chunk += static_cast<uint64_t>(gridDim.x) * kThreads) {
-        const uint64_t e0 = chunk * 8, b = chunk / 8;
+    auto scale_of = [&](uint64_t b) {
         float s;
         if constexpr (DQ) s = dq * e4m3_decode(scales_u8[b]);
         else s = scales_f32[b];
-        if (s == 0.0f || !__builtin_isfinite(s)) s = 1.0f;
-        const bool full = vec_ok && e0 + 8 <= n;
-        uint32_t word = 0;
-        if (full) {
-            word = *reinterpret_cast<const uint32_t *>(codes + chunk * 4);
-        } else {
-            const uint64_t nbytes = (n - e0 + 1) / 2;
-            for (uint64_t j = 0; j < 4 && j < nbytes; ++j)
-                word |= static_cast<uint32_t>(codes[chunk * 4 + j]) << (8 * j);
-        }
-        float o[8];
+        return (s == 0.0f || !__builtin_isfinite(s)) ? 1.0f : s;
+    };
+    const uint64_t ntiles = vec_ok ? n / kDecTile : 0;
+    int buf = 0;
+    for (uint64_t t = blockIdx.x; t < ntiles; t += gridDim.x, buf ^= 1) {
+        const uint64_t e0 = t * kDecTile + 16ull * threadIdx.x;
+        const uint2 w = *reinterpret_cast<const uint2 *>(codes + e0 / 2);
+        const float s = scale_of(e0 / kQuantBlock);
+        float *dst = tile[buf] + 16 * threadIdx.x;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t byte = (word >> (8 * j)) & 0xFFu;
-            o[2 * j] = s * L[byte >> 4];
-            o[2 * j + 1] = s * L[byte & 15u];
-        }
-        if (full) {
-            f32x4 *dst = reinterpret_cast<f32x4 *>(out + e0);
-            const f32x4 lo = {o[0], o[1], o[2], o[3]}, hi = {o[4], o[5], o[6], o[7]};
-            __builtin_nontemporal_store(lo, dst);
-            __builtin_nontemporal_store(hi, dst + 1);
-        } else {
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t word = h ? w.y : w.x;
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (e0 + i < n) out[e0 + i] = o[i];
+            for (int q = 0; q < 2; ++q) {
+                const uint32_t b0 = (word >> (16 * q)) & 0xFFu, b1 = (word >> (16 * q + 8)) & 0xFFu;
+                *reinterpret_cast<float4 *>(dst + 8 * h + 4 * q) =
+                    float4{s * L[b0 >> 4], s * L[b0 & 15u], s * L[b1 >> 4], s * L[b1 & 15u]};
+            }
         }
+        __syncthreads();
+        float4 *o = reinterpret_cast<float4 *>(out + t * kDecTile);
+        const float4 *src = reinterpret_cast<const float4 *>(tile[buf]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[threadIdx.x + kThreads * j] = src[threadIdx.x + kThreads * j];
+        // the next tile writes the other buffer; this one is reused two
+        // tiles later, after the barrier of the next tile
+    }
+    // tail (and unaligned sections): element by element
+    const uint64_t done = ntiles * kDecTile;
+    for (uint64_t e = done + static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; e < n;
+         e += static_cast<uint64_t>(gridDim.x) * kThreads) {
+        const uint8_t byte = codes[e >> 1];
+        const uint32_t code = (e & 1) ? (byte & 15u) : (byte >> 4);
+        out[e] = scale_of(e / kQuantBlock) * L[code];
     }
 }
 
 __global__ void nf4_code_batch_kernel(const float *__restrict__ v, uint64_t n, uint8_t *__restrict__ c) {
+    __shared__ Nf4Table tab;
+    nf4_table_build(tab);
+    __syncthreads();
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
-        c[i] = static_cast<uint8_t>(nf4_code(v[i]));
+        c[i] = static_cast<uint8_t>(nf4_code(tab, v[i]));
 }
 
 __global__ void e4m3_encode_batch_kernel(const float *__restrict__ v, uint64_t n, uint8_t *__restrict__ c) {
@@ -302,6 +373,8 @@ __global__ __launch_bounds__(kThreads) void nf4_code_sweep_kernel(uint64_t lo, u
                                                                   unsigned long long *__restrict__ hist,
                                                                   unsigned long long *__restrict__ checksum) {
     __shared__ unsigned int h[16];
+    __shared__ Nf4Table tab;
+    nf4_table_build(tab);
     if (threadIdx.x < 16) h[threadIdx.x] = 0;
     __syncthreads();
     unsigned long long cs = 0;
@@ -311,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void nf4_code_sweep_kernel(uint64_t lo, u
     for (uint64_t p = lo + static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; p < hi;
          p += static_cast<uint64_t>(gridDim.x) * kThreads) {
         const uint32_t bits = static_cast<uint32_t>(p);
-        const uint32_t c = nf4_code(__uint_as_float(bits));
+        const uint32_t c = nf4_code(tab, __uint_as_float(bits));
 #pragma unroll
         for (int i = 0; i < 16; ++i) hl[i] += (c == static_cast<uint32_t>(i)) ? 1u : 0u;
         cs += static_cast<unsigned long long>(c) * (bits % 65521u);
@@ -337,8 +410,9 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
                          float *dq_out, uint8_t *codes, uint32_t *gmax_scratch, hipStream_t stream) {
     BSQ_REQUIRE(n > 0, "quant encode: empty input");
     const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
-    const uint64_t nchunks = ceil_div(n, 8);
-    const unsigned grid = grid_for(nchunks);
+    // one chunk per thread until the grid reaches its cap (small sections keep
+    // every CU busy); the unrolled loop then covers the rest
+    const unsigned grid = grid_for(ceil_div(n, 8));
     if (method == kMethodNF4) {
         BSQ_REQUIRE(scales_f32 && codes, "quant encode: null NF4 output");
         quant_encode_kernel<false><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, scales_f32, nullptr, nullptr,
@@ -358,8 +432,8 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
 void launch_quant_decode(uint64_t n, int method, const float *scales_f32, const uint8_t *scales_u8,
                          const float *dq, const uint8_t *codes, float *out, hipStream_t stream) {
     BSQ_REQUIRE(n > 0, "quant decode: empty output");
-    const bool vec_ok = aligned16(out) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
-    const unsigned grid = grid_for(ceil_div(n, 8));
+    const bool vec_ok = aligned16(out) && ((reinterpret_cast<uintptr_t>(codes) & 7u) == 0);
+    const unsigned grid = grid_for(ceil_div(n, 16));
     if (method == kMethodNF4) {
         BSQ_REQUIRE(scales_f32 && codes, "quant decode: null NF4 input");
         quant_decode_kernel<false><<<grid, kThreads, 0, stream>>>(n, vec_ok, scales_f32, nullptr, nullptr, codes,

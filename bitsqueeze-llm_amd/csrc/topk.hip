@@ -60,6 +60,37 @@ __device__ __forceinline__ float load_value(const TopkArgs &a, const float *Ls, 
     }
 }
 
+// The values of the 4 consecutive elements e .. e + 3 (e % 4 == 0, the four
+// in one row and one 64-element block, a 16-byte aligned): one 16-byte load
+// of a (and of b), and for the NF4 sources one 2-byte code load and one block
+// scale, decoded exactly as load_value does element by element.
+template <TopkSource SRC>
+__device__ __forceinline__ void load_quad(const TopkArgs &a, const float *Ls, float dq, uint64_t e, float (&v)[4]) {
+    const float4 x = *reinterpret_cast<const float4 *>(a.a + e);
+    if constexpr (SRC == TopkSource::Dense) {
+        v[0] = x.x;
+        v[1] = x.y;
+        v[2] = x.z;
+        v[3] = x.w;
+    } else if constexpr (SRC == TopkSource::DenseMinusDense) {
+        const float4 y = *reinterpret_cast<const float4 *>(a.b + e);
+        v[0] = x.x - y.x;
+        v[1] = x.y - y.y;
+        v[2] = x.z - y.z;
+        v[3] = x.w - y.w;
+    } else {
+        float s;
+        if constexpr (SRC == TopkSource::DenseMinusNF4DQ) s = dq * e4m3_decode(a.scales_u8[e >> 6]);
+        else s = a.scales_f32[e >> 6];
+        if (s == 0.0f || !__builtin_isfinite(s)) s = 1.0f;
+        const uint32_t h = *reinterpret_cast<const uint16_t *>(a.codes + (e >> 1));
+        v[0] = x.x - s * Ls[(h >> 4) & 15u];
+        v[1] = x.y - s * Ls[h & 15u];
+        v[2] = x.z - s * Ls[(h >> 12) & 15u];
+        v[3] = x.w - s * Ls[(h >> 8) & 15u];
+    }
+}
+
 // Inclusive scan of one value per thread over the 256-thread workgroup.
 __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t *wsum) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -150,7 +181,10 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
     // test of device_buffer_has_nonzero (src/bitsqz_llm.cu:175-184, 396-423).
     bool nonzero = false;
     unsigned long long tmax = 0;  // largest composite key among this thread's columns
-    const bool vec4 = ((cols & 3u) == 0) && ((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0);
+    const bool vec4 = ((cols & 3u) == 0) && ((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0) &&
+                      (SRC != TopkSource::DenseMinusDense || (reinterpret_cast<uintptr_t>(a.b) & 15u) == 0) &&
+                      ((SRC != TopkSource::DenseMinusNF4 && SRC != TopkSource::DenseMinusNF4DQ) ||
+                       (reinterpret_cast<uintptr_t>(a.codes) & 1u) == 0);
     if constexpr (CACHED) {
         if (SRC == TopkSource::Dense && vec4) {
             // 16-byte loads, several in flight per lane: the row is read once
@@ -161,6 +195,22 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
                 const float4 v4 = src4[c4];
                 cache4[c4] = v4;
                 const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    nonzero |= fabsf(vv[u]) > FLT_EPSILON;
+                    const unsigned long long K = composite_key(vv[u], 4 * c4 + u);
+                    tmax = K > tmax ? K : tmax;
+                }
+            }
+        } else if (vec4) {
+            // the subtracting sources, 4 columns at a time (one 16-byte load
+            // of a, and of b or of two code bytes and the block scale)
+            float4 *cache4 = reinterpret_cast<float4 *>(cache);
+#pragma unroll 4
+            for (uint32_t c4 = threadIdx.x; c4 < cols / 4; c4 += kThreads) {
+                float vv[4];
+                load_quad<SRC>(a, sh.L, dq, row0 + 4 * c4, vv);
+                cache4[c4] = float4{vv[0], vv[1], vv[2], vv[3]};
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     nonzero |= fabsf(vv[u]) > FLT_EPSILON;
@@ -450,6 +500,8 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     }
     __syncthreads();
 
+    const bool quad_ok = (SRC != TopkSource::DenseMinusNF4 && SRC != TopkSource::DenseMinusNF4DQ) ||
+                         (reinterpret_cast<uintptr_t>(a.codes) & 1u) == 0;
     // the row: v[m][u] = column 4 (tid + 256 m) + u.  Absent columns (>= cols)
     // hold NaN: their composite keys are below every real entry's (NaN key 0,
     // and a smaller inverted column than any real NaN), so they never reach
@@ -465,6 +517,8 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
                 v[m][1] = x.y;
                 v[m][2] = x.z;
                 v[m][3] = x.w;
+            } else if (quad_ok) {
+                load_quad<SRC>(a, sh.L, dq, row0 + 4 * c4, v[m]);
             } else {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) v[m][u] = load_value<SRC>(a, sh.L, dq, row0 + 4 * c4 + u);

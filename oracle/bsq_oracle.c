@@ -345,3 +345,38 @@ ORACLE_API uint64_t oracle_nf4_threshold_mismatches(const float *T, uint64_t lo,
     }
     return bad;
 }
+
+/* Counts the floats with |v| < 2 in [lo, hi) where the 256-bin table rule of
+ * the device NF4 code function (bin b = clamp(int((v + 1) * 128), 0, 255),
+ * code = lo[b] + (v >= thr[b]), lo[b] = #{T_i <= -1 + b/128}, thr[b] the
+ * threshold inside bin b or +inf) disagrees with the reference's linear scan.
+ * The table is built with the same float arithmetic as the device. */
+ORACLE_API uint64_t oracle_nf4_table_mismatches(const float *T, uint64_t lo, uint64_t hi) {
+    float thr[256];
+    unsigned lowc[256];
+    for (int b = 0; b < 256; ++b) {
+        const float e0 = -1.0f + (float)b / 128.0f, e1 = -1.0f + (float)(b + 1) / 128.0f;
+        unsigned c = 0;
+        float t = INFINITY;
+        for (int i = 0; i < 15; ++i) {
+            c += (T[i] <= e0) ? 1u : 0u;
+            if (T[i] > e0 && T[i] < e1) t = T[i];
+        }
+        thr[b] = t;
+        lowc[b] = c;
+    }
+    uint64_t bad = 0;
+    int64_t p;
+#pragma omp parallel for reduction(+ : bad)
+    for (p = (int64_t)lo; p < (int64_t)hi; ++p) {
+        const uint32_t bits = (uint32_t)p;
+        float v;
+        memcpy(&v, &bits, 4);
+        if (!(fabsf(v) < 2.0f)) continue;
+        int b = (int)((v + 1.0f) * 128.0f);
+        b = b < 0 ? 0 : (b > 255 ? 255 : b);
+        const unsigned c = lowc[b] + ((v >= thr[b]) ? 1u : 0u);
+        if (c != oracle_nf4_code(v)) ++bad;
+    }
+    return bad;
+}

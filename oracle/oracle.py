@@ -91,6 +91,8 @@ def lib():
         L.oracle_nf4_levels.restype = ctypes.POINTER(ctypes.c_float)
         L.oracle_nf4_threshold_mismatches.restype = ctypes.c_uint64
         L.oracle_nf4_threshold_mismatches.argtypes = [P, U64, U64]
+        L.oracle_nf4_table_mismatches.restype = ctypes.c_uint64
+        L.oracle_nf4_table_mismatches.argtypes = [P, U64, U64]
         _lib = L
     return _lib
 
@@ -134,6 +136,14 @@ def nf4_threshold_mismatches(thresholds: np.ndarray, lo: int = 0, hi: int = 1 <<
     t = np.ascontiguousarray(thresholds, dtype=np.float32)
     assert t.size == 15
     return int(lib().oracle_nf4_threshold_mismatches(_p(t), lo, hi))
+
+
+def nf4_table_mismatches(thresholds: np.ndarray, lo: int = 0, hi: int = 1 << 32) -> int:
+    """Floats with |v| < 2 in [lo, hi) where the device's 256-bin table rule
+    differs from the scan."""
+    t = np.ascontiguousarray(thresholds, dtype=np.float32)
+    assert t.size == 15
+    return int(lib().oracle_nf4_table_mismatches(_p(t), lo, hi))
 
 
 @dataclass

@@ -166,6 +166,19 @@ def test_device_thresholds_pinned_against_reference_scan():
     assert O.nf4_threshold_mismatches(t) == 0
 
 
+def test_device_code_table_pinned_against_reference_scan():
+    """The device NF4 code function reads code = lo[b] + (v >= thr[b]) from a
+    256-bin table over [-1, 1] (clamped outside); built with the same float
+    arithmetic, the rule equals the reference's linear scan on every float
+    with |v| < 2 (2^31 bit patterns, CPU oracle)."""
+    from oracle import oracle as O
+    assert O.nf4_table_mismatches(B.nf4_thresholds()) == 0
+    # a plausible slip is caught: one threshold moved by one ulp
+    t = B.nf4_thresholds().copy()
+    t[7] = np.nextafter(t[7], np.float32(1.0))
+    assert O.nf4_table_mismatches(t) > 0
+
+
 def _valid_object() -> bytes:
     """A well-formed packed object (SVD sections U, S, V as NF4 / FP32 / NF4, an
     outlier blob), built by the oracle's byte-layout restatement."""
