@@ -147,9 +147,15 @@ struct Runtime {
     uint8_t *q_codes = nullptr;
     // last compress result, device-resident
     bsq_device_packed_t last{};
+    // pinned host staging of the packed payload (largest payload the
+    // configuration can produce, plus the Meta block): the sections move
+    // between HBM and the host object through it at full link speed
+    uint8_t *h_stage = nullptr;
+    uint64_t h_stage_bytes = 0;
 
     void release() noexcept {
         if (stream) (void)hipStreamSynchronize(stream);
+        if (h_stage) (void)hipHostFree(h_stage);
         for (auto &s : sec) s.release();
         for (auto &t : topk) t.release();
         dev_free(d_stage);
@@ -259,6 +265,36 @@ void create_stream(Runtime &rt) {
     BSQ_HIP(hipMemsetAsync(rt.meta, 0, sizeof(Meta), rt.stream));
 }
 
+uint64_t quant_section_bytes(int method, uint64_t count) {
+    if (method == kMethodNone) return count * 4;
+    const uint64_t nb = ceil_div(count, kQuantBlock);
+    return 48 + (method == kMethodNF4 ? nb * 4 : nb) + (count + 1) / 2;
+}
+
+// Largest payload of the runtime's configuration: its dense / quantised
+// sections and both top-k blobs at full capacity.
+uint64_t max_payload_bytes(const Runtime &rt) {
+    const uint64_t rows = rt.rows, cols = rt.cols;
+    uint64_t p = 0;
+    if (rt.svd_ranks >= 1) {
+        const uint64_t q = static_cast<uint64_t>(rt.q);
+        p += quant_section_bytes(rt.uv_fmt, rows * q) + quant_section_bytes(rt.s_fmt, q) +
+             quant_section_bytes(rt.uv_fmt, cols * q);
+    } else {
+        p += quant_section_bytes(rt.direct_fmt, rows * cols);
+    }
+    for (const auto &t : rt.topk)
+        if (t.capacity) p += 8 + rows * t.capacity * 6;
+    return p;
+}
+
+void alloc_host_stage(Runtime &rt) {
+    rt.h_stage_bytes = ceil_div(max_payload_bytes(rt), 256) * 256 + sizeof(Meta);
+    void *p = nullptr;
+    BSQ_HIP(hipHostMalloc(&p, rt.h_stage_bytes, hipHostMallocDefault));
+    rt.h_stage = static_cast<uint8_t *>(p);
+}
+
 // bitsqz_llm_compress_initialize body (src/bitsqz_llm.cu:785-885).
 void compress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int svd_ranks, int svd_niters,
                    int uv, int s, int direct, int loc) {
@@ -305,6 +341,7 @@ void compress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int s
         sc.count = N;
         if (sc.method != kMethodNone) sc.alloc_quant();
     }
+    alloc_host_stage(rt);
     BSQ_HIP(hipStreamSynchronize(rt.stream));
     rt.initialized = true;
 }
@@ -347,6 +384,7 @@ void decompress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int
     }
     if (r_out > 0.0f) init_topk(rt.topk[TK_OUTLIER], rows, cols, r_out);
     if (r_err > 0.0f) init_topk(rt.topk[TK_ERROR], rows, cols, r_err);
+    alloc_host_stage(rt);
     BSQ_HIP(hipStreamSynchronize(rt.stream));
     rt.initialized = true;
 }
@@ -570,11 +608,13 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
 // scatter (topk_cuda_utils.cuh:132-149), which the row-local fused scatter
 // does not reproduce.
 bool topk_blob_has_wide_index(const uint8_t *p, uint64_t n, uint32_t cols) {
-    const uint8_t *q = p + sizeof(uint16_t) * 4;
-    uint32_t mx = 0;  // a max-reduction (vectorisable), the blob may be unaligned
-    for (uint64_t i = 0; i < n; ++i) {
-        const uint32_t c = static_cast<uint32_t>(q[2 * i]) | (static_cast<uint32_t>(q[2 * i + 1]) << 8);
-        mx = c > mx ? c : mx;
+    const uint8_t *q = p + sizeof(uint16_t) * 4;  // the indices (the blob may sit at any byte offset)
+    uint16_t chunk[4096];
+    uint16_t mx = 0;
+    for (uint64_t i0 = 0; i0 < n; i0 += 4096) {
+        const uint64_t m = std::min<uint64_t>(4096, n - i0);
+        std::memcpy(chunk, q + 2 * i0, m * 2);
+        for (uint64_t i = 0; i < m; ++i) mx = chunk[i] > mx ? chunk[i] : mx;  // vectorised max
     }
     return n > 0 && mx >= cols;
 }
@@ -603,65 +643,79 @@ static_assert(sizeof(bitsqz_llm_array_t) == 200, "bitsqz_llm_array_t must be 200
 static_assert(offsetof(bitsqz_llm_array_t, section_u) == 48, "section_u offset");
 static_assert(offsetof(bitsqz_llm_array_t, payload) == 192, "payload offset");
 
+// The host packed object (src/bitsqz_llm.cu:1237-1277): every section part
+// goes device -> pinned staging at its final payload offset (the error blob
+// last, so its presence, decided on the device, only shortens the payload),
+// then one host copy fills the caller's calloc block.
 bitsqz_llm_array_t *assemble_host(Runtime &rt, const bsq_device_packed_t &P) {
     const hipStream_t st = rt.stream;
-    Meta meta{};
-    BSQ_HIP(hipMemcpyAsync(&meta, rt.meta, sizeof(Meta), hipMemcpyDeviceToHost, st));
-    BSQ_HIP(hipStreamSynchronize(st));
     bitsqz_llm_array_t H = P.header;
+    const bitsqz_section_t *descs[6] = {&H.section_u, &H.section_s, &H.section_v, &H.section_direct,
+                                        &H.section_outlier_topk, &H.section_error_topk};
+    uint64_t full = 0;  // payload bytes with the error blob
+    for (auto *d : descs)
+        if (d->storage != BITSQZ_SECTION_NONE) full = std::max(full, d->offset + d->size);
+    BSQ_REQUIRE(full + sizeof(Meta) <= rt.h_stage_bytes, "packed payload larger than the host staging");
+    uint8_t *stage = rt.h_stage;
+    Meta *hmeta = reinterpret_cast<Meta *>(stage + rt.h_stage_bytes - sizeof(Meta));
+    for (int i = 0; i < 4; ++i) {
+        const bitsqz_section_t &d = *descs[i];
+        if (d.storage == BITSQZ_SECTION_NONE) continue;
+        uint8_t *dst = stage + d.offset;
+        if (d.storage == BITSQZ_SECTION_FP32) {
+            BSQ_HIP(hipMemcpyAsync(dst, P.d_dense[i], P.count[i] * 4, hipMemcpyDeviceToHost, st));
+            continue;
+        }
+        const int method = (i == SEC_S) ? H.svd_s_format : (i == SEC_DIRECT ? H.quantization_only_format
+                                                                             : H.svd_uv_format);
+        const uint64_t nb = ceil_div(P.count[i], kQuantBlock);
+        const uint64_t ssz = method == kMethodNF4 ? nb * 4 : nb;
+        const void *ssrc = method == kMethodNF4 ? static_cast<const void *>(P.d_scales_f32[i])
+                                                : static_cast<const void *>(P.d_scales_u8[i]);
+        BSQ_HIP(hipMemcpyAsync(dst + 48, ssrc, ssz, hipMemcpyDeviceToHost, st));
+        BSQ_HIP(hipMemcpyAsync(dst + 48 + ssz, P.d_codes[i], (P.count[i] + 1) / 2, hipMemcpyDeviceToHost, st));
+    }
+    for (int t = 0; t < 2; ++t) {
+        const bitsqz_section_t &d = *descs[4 + t];
+        if (d.storage == BITSQZ_SECTION_NONE) continue;
+        const uint64_t n = static_cast<uint64_t>(H.num_rows) * P.topk_k[t];
+        BSQ_HIP(hipMemcpyAsync(stage + d.offset + 8, P.d_topk_idx[t], n * 2, hipMemcpyDeviceToHost, st));
+        BSQ_HIP(hipMemcpyAsync(stage + d.offset + 8 + n * 2, P.d_topk_val[t], n * 4, hipMemcpyDeviceToHost, st));
+    }
+    BSQ_HIP(hipMemcpyAsync(hmeta, rt.meta, sizeof(Meta), hipMemcpyDeviceToHost, st));
+    BSQ_HIP(hipStreamSynchronize(st));
+    const Meta meta = *hmeta;
     const bool err_present = P.topk_k[1] > 0 && (meta.flags & kFlagError);
     if (err_present) H.flags |= kFlagError;
     else H.section_error_topk = bitsqz_section_t{};
     uint64_t payload = 0;
-    const bitsqz_section_t *descs[6] = {&H.section_u, &H.section_s, &H.section_v, &H.section_direct,
-                                        &H.section_outlier_topk, &H.section_error_topk};
     for (auto *d : descs)
         if (d->storage != BITSQZ_SECTION_NONE) payload = std::max(payload, d->offset + d->size);
+    // the host-written headers of the quantised sections and top-k blobs
+    for (int i = 0; i < 4; ++i) {
+        const bitsqz_section_t &d = *descs[i];
+        if (d.storage != BITSQZ_SECTION_QUANT) continue;
+        const int method = (i == SEC_S) ? H.svd_s_format : (i == SEC_DIRECT ? H.quantization_only_format
+                                                                             : H.svd_uv_format);
+        QuantHeader qh{};
+        qh.magic = kQuantMagic;
+        qh.version = kQuantVersion;
+        qh.method = method;
+        qh.num_elements = P.count[i];
+        qh.num_blocks = ceil_div(P.count[i], kQuantBlock);
+        qh.block_size = kQuantBlock;
+        qh.dq_scale = method == kMethodNF4DQ ? meta.dq[i] : 0.0f;
+        std::memcpy(stage + d.offset, &qh, sizeof(qh));
+    }
+    for (int t = 0; t < 2; ++t) {
+        const bitsqz_section_t &d = *descs[4 + t];
+        if (d.storage == BITSQZ_SECTION_NONE) continue;
+        const TopkHeader th{H.num_rows, H.num_columns, P.topk_k[t], 0};
+        std::memcpy(stage + d.offset, &th, sizeof(th));
+    }
     auto *buf = static_cast<bitsqz_llm_array_t *>(std::calloc(1, 200 + payload));
     BSQ_REQUIRE(buf != nullptr, "calloc of the packed object failed");
-    try {
-        uint8_t *pl = reinterpret_cast<uint8_t *>(buf) + 200;
-        for (int i = 0; i < 4; ++i) {
-            const bitsqz_section_t &d = *descs[i];
-            if (d.storage == BITSQZ_SECTION_NONE) continue;
-            uint8_t *dst = pl + d.offset;
-            if (d.storage == BITSQZ_SECTION_FP32) {
-                BSQ_HIP(hipMemcpyAsync(dst, P.d_dense[i], P.count[i] * 4, hipMemcpyDeviceToHost, st));
-                continue;
-            }
-            const int method = (i == SEC_S) ? H.svd_s_format : (i == SEC_DIRECT ? H.quantization_only_format
-                                                                                 : H.svd_uv_format);
-            const uint64_t nb = ceil_div(P.count[i], kQuantBlock);
-            QuantHeader qh{};
-            qh.magic = kQuantMagic;
-            qh.version = kQuantVersion;
-            qh.method = method;
-            qh.num_elements = P.count[i];
-            qh.num_blocks = nb;
-            qh.block_size = kQuantBlock;
-            qh.dq_scale = method == kMethodNF4DQ ? meta.dq[i] : 0.0f;
-            std::memcpy(dst, &qh, sizeof(qh));
-            const uint64_t ssz = method == kMethodNF4 ? nb * 4 : nb;
-            const void *ssrc = method == kMethodNF4 ? static_cast<const void *>(P.d_scales_f32[i])
-                                                    : static_cast<const void *>(P.d_scales_u8[i]);
-            BSQ_HIP(hipMemcpyAsync(dst + 48, ssrc, ssz, hipMemcpyDeviceToHost, st));
-            BSQ_HIP(hipMemcpyAsync(dst + 48 + ssz, P.d_codes[i], (P.count[i] + 1) / 2, hipMemcpyDeviceToHost, st));
-        }
-        for (int t = 0; t < 2; ++t) {
-            const bitsqz_section_t &d = *descs[4 + t];
-            if (d.storage == BITSQZ_SECTION_NONE) continue;
-            uint8_t *dst = pl + d.offset;
-            TopkHeader th{H.num_rows, H.num_columns, P.topk_k[t], 0};
-            std::memcpy(dst, &th, sizeof(th));
-            const uint64_t n = static_cast<uint64_t>(H.num_rows) * P.topk_k[t];
-            BSQ_HIP(hipMemcpyAsync(dst + 8, P.d_topk_idx[t], n * 2, hipMemcpyDeviceToHost, st));
-            BSQ_HIP(hipMemcpyAsync(dst + 8 + n * 2, P.d_topk_val[t], n * 4, hipMemcpyDeviceToHost, st));
-        }
-        BSQ_HIP(hipStreamSynchronize(st));
-    } catch (...) {
-        std::free(buf);
-        throw;
-    }
+    std::memcpy(reinterpret_cast<uint8_t *>(buf) + 200, stage, payload);
     std::memcpy(buf, &H, sizeof(H));
     buf->payload = reinterpret_cast<uint8_t *>(buf) + 200;
     return buf;
@@ -781,7 +835,16 @@ bool quant_blob_ok(const uint8_t *p, uint64_t size, int method, uint64_t count, 
 // and topk_unpack_from_buffer (src/bitsqz_llm.cu:539-607, topk_cuda.cu:332-383).
 void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
     const hipStream_t st = rt.stream;
+    // the caller's payload is pageable host memory: one host copy into the
+    // pinned staging, then every host -> device copy runs at full link speed
+    // (payloads larger than the staging, e.g. an FP32 direct section in a
+    // runtime configured for another path, are copied from where they lie)
     const uint8_t *pl = static_cast<const uint8_t *>(c->payload);
+    const uint64_t payload_bytes = bitsqz_llm_get_packed_size(c) - sizeof(bitsqz_llm_array_t);
+    if (rt.h_stage && payload_bytes <= rt.h_stage_bytes - sizeof(Meta)) {
+        std::memcpy(rt.h_stage, pl, payload_bytes);
+        pl = rt.h_stage;
+    }
     bsq_device_packed_t P{};
     P.header = *c;
     const uint32_t rows = c->num_rows, cols = c->num_columns;
