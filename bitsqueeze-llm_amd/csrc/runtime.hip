@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <limits>
+#include <memory>
 #include <vector>
 
 namespace bsq {
@@ -133,6 +134,11 @@ struct Runtime {
 
     hipStream_t stream = nullptr;
     hipEvent_t ev[8] = {};
+    // payload copies between HBM and the pinned staging run on their own
+    // stream (default priority), ordered after their producers by events, so
+    // they overlap the compute stream's remaining work
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t cev[4] = {};
     float *d_stage = nullptr;     // HOST-input staging
     float *d_residual = nullptr;  // input with outliers zeroed
     float *d_err = nullptr;       // residual - U S V^T (SVD path with error top-k)
@@ -155,6 +161,7 @@ struct Runtime {
 
     void release() noexcept {
         if (stream) (void)hipStreamSynchronize(stream);
+        if (copy_stream) (void)hipStreamSynchronize(copy_stream);
         if (h_stage) (void)hipHostFree(h_stage);
         for (auto &s : sec) s.release();
         for (auto &t : topk) t.release();
@@ -169,7 +176,10 @@ struct Runtime {
         svd = nullptr;
         for (auto &e : ev)
             if (e) (void)hipEventDestroy(e);
+        for (auto &e : cev)
+            if (e) (void)hipEventDestroy(e);
         if (stream) (void)hipStreamDestroy(stream);
+        if (copy_stream) (void)hipStreamDestroy(copy_stream);
         *this = Runtime{};
     }
 };
@@ -260,7 +270,9 @@ void init_topk(TopkBuf &t, uint16_t rows, uint16_t cols, float ratio) {
 
 void create_stream(Runtime &rt) {
     BSQ_HIP(hipStreamCreateWithFlags(&rt.stream, hipStreamNonBlocking));
+    BSQ_HIP(hipStreamCreateWithFlags(&rt.copy_stream, hipStreamNonBlocking));
     for (auto &e : rt.ev) BSQ_HIP(hipEventCreate(&e));
+    for (auto &e : rt.cev) BSQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     rt.meta = dev_alloc<Meta>(1);
     BSQ_HIP(hipMemsetAsync(rt.meta, 0, sizeof(Meta), rt.stream));
 }
@@ -289,7 +301,7 @@ uint64_t max_payload_bytes(const Runtime &rt) {
 }
 
 void alloc_host_stage(Runtime &rt) {
-    rt.h_stage_bytes = ceil_div(max_payload_bytes(rt), 256) * 256 + sizeof(Meta);
+    rt.h_stage_bytes = ceil_div(max_payload_bytes(rt), 256) * 256 + 2 * sizeof(Meta);
     void *p = nullptr;
     BSQ_HIP(hipHostMalloc(&p, rt.h_stage_bytes, hipHostMallocDefault));
     rt.h_stage = static_cast<uint8_t *>(p);
@@ -643,79 +655,116 @@ static_assert(sizeof(bitsqz_llm_array_t) == 200, "bitsqz_llm_array_t must be 200
 static_assert(offsetof(bitsqz_llm_array_t, section_u) == 48, "section_u offset");
 static_assert(offsetof(bitsqz_llm_array_t, payload) == 192, "payload offset");
 
-// The host packed object (src/bitsqz_llm.cu:1237-1277): every section part
-// goes device -> pinned staging at its final payload offset (the error blob
-// last, so its presence, decided on the device, only shortens the payload),
-// then one host copy fills the caller's calloc block.
+// The host packed object (src/bitsqz_llm.cu:1237-1277).  Every section part
+// goes device -> pinned staging at its final payload offset, in three groups
+// on the copy stream, each as soon as its producer has run: the outlier blob
+// after the separation, the dense / quantised sections after the encode, the
+// error blob (whose presence the device decides) after the last kernel.  The
+// host fills the caller's calloc block group by group, so only the last
+// group's copies follow the compute.
 bitsqz_llm_array_t *assemble_host(Runtime &rt, const bsq_device_packed_t &P) {
-    const hipStream_t st = rt.stream;
+    const hipStream_t cs = rt.copy_stream;
     bitsqz_llm_array_t H = P.header;
     const bitsqz_section_t *descs[6] = {&H.section_u, &H.section_s, &H.section_v, &H.section_direct,
                                         &H.section_outlier_topk, &H.section_error_topk};
     uint64_t full = 0;  // payload bytes with the error blob
     for (auto *d : descs)
         if (d->storage != BITSQZ_SECTION_NONE) full = std::max(full, d->offset + d->size);
-    BSQ_REQUIRE(full + sizeof(Meta) <= rt.h_stage_bytes, "packed payload larger than the host staging");
+    BSQ_REQUIRE(full + 2 * sizeof(Meta) <= rt.h_stage_bytes, "packed payload larger than the host staging");
+    // the staging holds every part at its final payload offset, plus two
+    // snapshots of the Meta block (dq scales after the encode, flags at the end)
     uint8_t *stage = rt.h_stage;
-    Meta *hmeta = reinterpret_cast<Meta *>(stage + rt.h_stage_bytes - sizeof(Meta));
+    Meta *meta_sec = reinterpret_cast<Meta *>(stage + rt.h_stage_bytes - 2 * sizeof(Meta));
+    Meta *meta_end = reinterpret_cast<Meta *>(stage + rt.h_stage_bytes - sizeof(Meta));
+    auto copy_topk = [&](int t) {
+        const bitsqz_section_t &d = *descs[4 + t];
+        if (d.storage == BITSQZ_SECTION_NONE) return;
+        const uint64_t n = static_cast<uint64_t>(H.num_rows) * P.topk_k[t];
+        BSQ_HIP(hipMemcpyAsync(stage + d.offset + 8, P.d_topk_idx[t], n * 2, hipMemcpyDeviceToHost, cs));
+        BSQ_HIP(hipMemcpyAsync(stage + d.offset + 8 + n * 2, P.d_topk_val[t], n * 4, hipMemcpyDeviceToHost, cs));
+    };
+    auto section_method = [&](int i) {
+        return (i == SEC_S) ? H.svd_s_format : (i == SEC_DIRECT ? H.quantization_only_format : H.svd_uv_format);
+    };
+    // group 0: the outlier blob, final once the separation has run (ev[1])
+    BSQ_HIP(hipStreamWaitEvent(cs, rt.ev[1], 0));
+    copy_topk(0);
+    BSQ_HIP(hipEventRecord(rt.cev[0], cs));
+    // group 1: U, S, V or the direct section, final after the encode (ev[3])
+    BSQ_HIP(hipStreamWaitEvent(cs, rt.ev[3], 0));
     for (int i = 0; i < 4; ++i) {
         const bitsqz_section_t &d = *descs[i];
         if (d.storage == BITSQZ_SECTION_NONE) continue;
         uint8_t *dst = stage + d.offset;
         if (d.storage == BITSQZ_SECTION_FP32) {
-            BSQ_HIP(hipMemcpyAsync(dst, P.d_dense[i], P.count[i] * 4, hipMemcpyDeviceToHost, st));
+            BSQ_HIP(hipMemcpyAsync(dst, P.d_dense[i], P.count[i] * 4, hipMemcpyDeviceToHost, cs));
             continue;
         }
-        const int method = (i == SEC_S) ? H.svd_s_format : (i == SEC_DIRECT ? H.quantization_only_format
-                                                                             : H.svd_uv_format);
+        const int method = section_method(i);
         const uint64_t nb = ceil_div(P.count[i], kQuantBlock);
         const uint64_t ssz = method == kMethodNF4 ? nb * 4 : nb;
         const void *ssrc = method == kMethodNF4 ? static_cast<const void *>(P.d_scales_f32[i])
                                                 : static_cast<const void *>(P.d_scales_u8[i]);
-        BSQ_HIP(hipMemcpyAsync(dst + 48, ssrc, ssz, hipMemcpyDeviceToHost, st));
-        BSQ_HIP(hipMemcpyAsync(dst + 48 + ssz, P.d_codes[i], (P.count[i] + 1) / 2, hipMemcpyDeviceToHost, st));
+        BSQ_HIP(hipMemcpyAsync(dst + 48, ssrc, ssz, hipMemcpyDeviceToHost, cs));
+        BSQ_HIP(hipMemcpyAsync(dst + 48 + ssz, P.d_codes[i], (P.count[i] + 1) / 2, hipMemcpyDeviceToHost, cs));
     }
-    for (int t = 0; t < 2; ++t) {
+    BSQ_HIP(hipMemcpyAsync(meta_sec, rt.meta, sizeof(Meta), hipMemcpyDeviceToHost, cs));
+    BSQ_HIP(hipEventRecord(rt.cev[1], cs));
+    // group 2: the error blob and the final flags, after the last kernel (ev[6])
+    BSQ_HIP(hipStreamWaitEvent(cs, rt.ev[6], 0));
+    copy_topk(1);
+    BSQ_HIP(hipMemcpyAsync(meta_end, rt.meta, sizeof(Meta), hipMemcpyDeviceToHost, cs));
+    BSQ_HIP(hipEventRecord(rt.cev[2], cs));
+
+    // the host object, sized for every section (the error blob's presence is
+    // decided last; a smaller object leaves the tail unused), filled group by
+    // group while the device still works on the later ones
+    std::unique_ptr<void, void (*)(void *)> block(std::calloc(1, 200 + full), std::free);
+    BSQ_REQUIRE(block != nullptr, "calloc of the packed object failed");
+    uint8_t *pl = static_cast<uint8_t *>(block.get()) + 200;
+    auto put_topk = [&](int t) {
         const bitsqz_section_t &d = *descs[4 + t];
-        if (d.storage == BITSQZ_SECTION_NONE) continue;
-        const uint64_t n = static_cast<uint64_t>(H.num_rows) * P.topk_k[t];
-        BSQ_HIP(hipMemcpyAsync(stage + d.offset + 8, P.d_topk_idx[t], n * 2, hipMemcpyDeviceToHost, st));
-        BSQ_HIP(hipMemcpyAsync(stage + d.offset + 8 + n * 2, P.d_topk_val[t], n * 4, hipMemcpyDeviceToHost, st));
-    }
-    BSQ_HIP(hipMemcpyAsync(hmeta, rt.meta, sizeof(Meta), hipMemcpyDeviceToHost, st));
-    BSQ_HIP(hipStreamSynchronize(st));
-    const Meta meta = *hmeta;
-    const bool err_present = P.topk_k[1] > 0 && (meta.flags & kFlagError);
-    if (err_present) H.flags |= kFlagError;
-    else H.section_error_topk = bitsqz_section_t{};
-    uint64_t payload = 0;
-    for (auto *d : descs)
-        if (d->storage != BITSQZ_SECTION_NONE) payload = std::max(payload, d->offset + d->size);
-    // the host-written headers of the quantised sections and top-k blobs
+        if (d.storage == BITSQZ_SECTION_NONE) return;
+        const TopkHeader th{H.num_rows, H.num_columns, P.topk_k[t], 0};
+        std::memcpy(pl + d.offset, &th, sizeof(th));
+        std::memcpy(pl + d.offset + 8, stage + d.offset + 8, d.size - 8);
+    };
+    BSQ_HIP(hipEventSynchronize(rt.cev[0]));
+    put_topk(0);
+    BSQ_HIP(hipEventSynchronize(rt.cev[1]));
+    const Meta msec = *meta_sec;
     for (int i = 0; i < 4; ++i) {
         const bitsqz_section_t &d = *descs[i];
-        if (d.storage != BITSQZ_SECTION_QUANT) continue;
-        const int method = (i == SEC_S) ? H.svd_s_format : (i == SEC_DIRECT ? H.quantization_only_format
-                                                                             : H.svd_uv_format);
-        QuantHeader qh{};
-        qh.magic = kQuantMagic;
-        qh.version = kQuantVersion;
-        qh.method = method;
-        qh.num_elements = P.count[i];
-        qh.num_blocks = ceil_div(P.count[i], kQuantBlock);
-        qh.block_size = kQuantBlock;
-        qh.dq_scale = method == kMethodNF4DQ ? meta.dq[i] : 0.0f;
-        std::memcpy(stage + d.offset, &qh, sizeof(qh));
-    }
-    for (int t = 0; t < 2; ++t) {
-        const bitsqz_section_t &d = *descs[4 + t];
         if (d.storage == BITSQZ_SECTION_NONE) continue;
-        const TopkHeader th{H.num_rows, H.num_columns, P.topk_k[t], 0};
-        std::memcpy(stage + d.offset, &th, sizeof(th));
+        if (d.storage == BITSQZ_SECTION_QUANT) {
+            const int method = section_method(i);
+            QuantHeader qh{};
+            qh.magic = kQuantMagic;
+            qh.version = kQuantVersion;
+            qh.method = method;
+            qh.num_elements = P.count[i];
+            qh.num_blocks = ceil_div(P.count[i], kQuantBlock);
+            qh.block_size = kQuantBlock;
+            qh.dq_scale = method == kMethodNF4DQ ? msec.dq[i] : 0.0f;
+            std::memcpy(pl + d.offset, &qh, sizeof(qh));
+            std::memcpy(pl + d.offset + 48, stage + d.offset + 48, d.size - 48);
+        } else {
+            std::memcpy(pl + d.offset, stage + d.offset, d.size);
+        }
     }
-    auto *buf = static_cast<bitsqz_llm_array_t *>(std::calloc(1, 200 + payload));
-    BSQ_REQUIRE(buf != nullptr, "calloc of the packed object failed");
-    std::memcpy(reinterpret_cast<uint8_t *>(buf) + 200, stage, payload);
+    // first touch of the error blob's pages (calloc maps them lazily) while
+    // the device still computes it, so the page faults stay off the tail
+    if (descs[5]->storage != BITSQZ_SECTION_NONE) std::memset(pl + descs[5]->offset, 0, descs[5]->size);
+    BSQ_HIP(hipEventSynchronize(rt.cev[2]));
+    const Meta mend = *meta_end;
+    const bool err_present = P.topk_k[1] > 0 && (mend.flags & kFlagError);
+    if (err_present) {
+        H.flags |= kFlagError;
+        put_topk(1);
+    } else {
+        H.section_error_topk = bitsqz_section_t{};
+    }
+    auto *buf = static_cast<bitsqz_llm_array_t *>(block.release());
     std::memcpy(buf, &H, sizeof(H));
     buf->payload = reinterpret_cast<uint8_t *>(buf) + 200;
     return buf;
@@ -834,24 +883,49 @@ bool quant_blob_ok(const uint8_t *p, uint64_t size, int method, uint64_t count, 
 // device descriptor for decompress_device.  Mirrors decode_section_to_device
 // and topk_unpack_from_buffer (src/bitsqz_llm.cu:539-607, topk_cuda.cu:332-383).
 void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
-    const hipStream_t st = rt.stream;
-    // the caller's payload is pageable host memory: one host copy into the
-    // pinned staging, then every host -> device copy runs at full link speed
-    // (payloads larger than the staging, e.g. an FP32 direct section in a
-    // runtime configured for another path, are copied from where they lie)
-    const uint8_t *pl = static_cast<const uint8_t *>(c->payload);
-    const uint64_t payload_bytes = bitsqz_llm_get_packed_size(c) - sizeof(bitsqz_llm_array_t);
-    if (rt.h_stage && payload_bytes <= rt.h_stage_bytes - sizeof(Meta)) {
-        std::memcpy(rt.h_stage, pl, payload_bytes);
-        pl = rt.h_stage;
-    }
+    const hipStream_t st = rt.stream, cs = rt.copy_stream;
+    // The caller's payload is pageable host memory.  Each section is copied by
+    // the host into the pinned staging (same offset) and moves to the device
+    // from there at full link speed; a section that does not fit the staging
+    // (e.g. an FP32 direct section in a runtime configured for another path)
+    // is copied from where it lies.  The dense sections go first, on the
+    // compute stream; the top-k blobs follow on the copy stream while the
+    // device decodes and reconstructs, and the scatter waits for them.
+    const uint8_t *src = static_cast<const uint8_t *>(c->payload);
+    const uint64_t stage_cap = rt.h_stage ? rt.h_stage_bytes - 2 * sizeof(Meta) : 0;
+    auto staged = [&](const bitsqz_section_t &s) -> const uint8_t * {
+        if (s.offset + s.size > stage_cap) return src;
+        std::memcpy(rt.h_stage + s.offset, src + s.offset, s.size);
+        return rt.h_stage;
+    };
     bsq_device_packed_t P{};
     P.header = *c;
     const uint32_t rows = c->num_rows, cols = c->num_columns;
     const uint64_t N = static_cast<uint64_t>(rows) * cols;
+
+    // top-k blobs: validated before anything is enqueued
+    const bitsqz_section_t *tsec[2] = {&c->section_outlier_topk, &c->section_error_topk};
+    const uint32_t tflag[2] = {kFlagOutlier, kFlagError};
+    uint64_t tn[2] = {0, 0};
+    bool tpresent[2] = {false, false}, wide = false;
+    for (int t = 0; t < 2; ++t) {
+        if (!(c->flags & tflag[t])) continue;
+        BSQ_REQUIRE(rt.topk[t].capacity > 0, "top-k runtime missing");
+        TopkHeader h;
+        BSQ_REQUIRE(topk_blob_ok(src + tsec[t]->offset, tsec[t]->size, &h), "invalid top-k section");
+        BSQ_REQUIRE(h.num_rows == rows && h.num_columns == cols && h.num_topk_columns <= rt.topk[t].capacity,
+                    "top-k section incompatible with the runtime");
+        tpresent[t] = true;
+        tn[t] = static_cast<uint64_t>(rows) * h.num_topk_columns;
+        P.d_topk_idx[t] = rt.topk[t].idx;
+        P.d_topk_val[t] = rt.topk[t].val;
+        P.topk_k[t] = h.num_topk_columns;
+    }
+
     auto stage_section = [&](int i, const bitsqz_section_t &s, int method, uint64_t count, float *dense_dst) {
         if (s.storage == BITSQZ_SECTION_FP32) {
             BSQ_REQUIRE(s.size == count * 4, "FP32 section size mismatch");
+            const uint8_t *pl = staged(s);
             BSQ_HIP(hipMemcpyAsync(dense_dst, pl + s.offset, count * 4, hipMemcpyHostToDevice, st));
             P.d_dense[i] = dense_dst;
             P.count[i] = count;
@@ -860,7 +934,8 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         BSQ_REQUIRE(s.storage == BITSQZ_SECTION_QUANT && method != kMethodNone, "bad quantised section");
         BSQ_REQUIRE(rt.quant_initialized, "quantisation runtime missing");
         QuantHeader h;
-        BSQ_REQUIRE(quant_blob_ok(pl + s.offset, s.size, method, count, &h), "invalid quantised section");
+        BSQ_REQUIRE(quant_blob_ok(src + s.offset, s.size, method, count, &h), "invalid quantised section");
+        const uint8_t *pl = staged(s);
         const uint64_t nb = h.num_blocks;
         const uint64_t ssz = method == kMethodNF4 ? nb * 4 : nb;
         void *sdst = method == kMethodNF4 ? static_cast<void *>(rt.q_scales_f32) : static_cast<void *>(rt.q_scales_u8);
@@ -879,40 +954,33 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         stage_section(SEC_U, c->section_u, c->svd_uv_format, static_cast<uint64_t>(rows) * q, rt.sec[SEC_U].dense);
         stage_section(SEC_S, c->section_s, c->svd_s_format, q, rt.sec[SEC_S].dense);
         stage_section(SEC_V, c->section_v, c->svd_uv_format, static_cast<uint64_t>(cols) * q, rt.sec[SEC_V].dense);
+        decompress_device(rt, P, false, d_dst, st, nullptr, false);  // the reconstruction (scatter below)
     } else {
         stage_section(SEC_DIRECT, c->section_direct, c->quantization_only_format, N, d_dst);
         P.d_dense[SEC_DIRECT] = nullptr;  // already decoded into d_dst
     }
-    bool has_err = false, wide = false;
-    const bitsqz_section_t *tsec[2] = {&c->section_outlier_topk, &c->section_error_topk};
-    const uint32_t tflag[2] = {kFlagOutlier, kFlagError};
-    for (int t = 0; t < 2; ++t) {
-        if (!(c->flags & tflag[t])) continue;
-        TopkBuf &tb = rt.topk[t];
-        BSQ_REQUIRE(tb.capacity > 0, "top-k runtime missing");
-        TopkHeader h;
-        BSQ_REQUIRE(topk_blob_ok(pl + tsec[t]->offset, tsec[t]->size, &h), "invalid top-k section");
-        BSQ_REQUIRE(h.num_rows == rows && h.num_columns == cols && h.num_topk_columns <= tb.capacity,
-                    "top-k section incompatible with the runtime");
-        const uint64_t n = static_cast<uint64_t>(rows) * h.num_topk_columns;
-        if (n > 0) {
-            BSQ_HIP(hipMemcpyAsync(tb.idx, pl + tsec[t]->offset + 8, n * 2, hipMemcpyHostToDevice, st));
-            BSQ_HIP(hipMemcpyAsync(tb.val, pl + tsec[t]->offset + 8 + n * 2, n * 4, hipMemcpyHostToDevice, st));
+
+    // top-k blobs: host copy and H2D overlap the decode / reconstruction
+    if (tpresent[0] || tpresent[1]) {
+        for (int t = 0; t < 2; ++t) {
+            if (!tpresent[t] || tn[t] == 0) continue;
+            const uint8_t *pl = staged(*tsec[t]);
+            BSQ_HIP(hipMemcpyAsync(rt.topk[t].idx, pl + tsec[t]->offset + 8, tn[t] * 2, hipMemcpyHostToDevice, cs));
+            BSQ_HIP(hipMemcpyAsync(rt.topk[t].val, pl + tsec[t]->offset + 8 + tn[t] * 2, tn[t] * 4,
+                                   hipMemcpyHostToDevice, cs));
+            // the scatter's form (in-row or flat positions) from the copy just made
+            wide = wide || topk_blob_has_wide_index(pl + tsec[t]->offset, tn[t], cols);
         }
-        P.d_topk_idx[t] = tb.idx;
-        P.d_topk_val[t] = tb.val;
-        P.topk_k[t] = h.num_topk_columns;
-        if (t == 1) has_err = true;
-        wide = wide || topk_blob_has_wide_index(pl + tsec[t]->offset, n, cols);
+        BSQ_HIP(hipEventRecord(rt.cev[3], cs));
+        BSQ_HIP(hipStreamWaitEvent(st, rt.cev[3], 0));
     }
-    const bool has_out = (c->flags & kFlagOutlier) != 0;
-    if (c->flags & kFlagSvd) decompress_device(rt, P, has_err, d_dst, st, nullptr, !wide);
+    const bool has_err = tpresent[1], has_out = tpresent[0];
     if (wide) {
         // the reference's two launches: the error set, then the outlier set
         // (src/bitsqz_llm.cu:1373-1387), each at flat positions
         if (has_err) launch_topk_scatter_flat(P.d_topk_idx[1], P.d_topk_val[1], P.topk_k[1], rows, cols, d_dst, st);
         if (has_out) launch_topk_scatter_flat(P.d_topk_idx[0], P.d_topk_val[0], P.topk_k[0], rows, cols, d_dst, st);
-    } else if (!(c->flags & kFlagSvd)) {
+    } else {
         launch_topk_scatter(P.d_topk_idx[1], P.d_topk_val[1], has_err ? P.topk_k[1] : 0, P.d_topk_idx[0],
                             P.d_topk_val[0], has_out ? P.topk_k[0] : 0, rows, cols, d_dst, true, st);
     }
