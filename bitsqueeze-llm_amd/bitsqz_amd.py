@@ -130,6 +130,7 @@ def lib():
         "bsq_kernel_timer_start": (i32, []),
         "bsq_copy_kernel": (i32, [P, P, u64, P]),
         "bsq_kernel_timer_stop": (i32, [C.POINTER(C.c_double), C.POINTER(i32)]),
+        "bsq_kernel_timer_read": (i32, [i32, C.POINTER(C.c_double), C.POINTER(i32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -204,15 +205,25 @@ class DeviceBuffer:
             pass
 
 
+TIMER_RECONSTRUCT, TIMER_RANGE_FINDER = 0, 1
+
+
 def kernel_timer_start() -> None:
-    """Bracket every reconstruction GEMM of the pipelines with HIP events."""
+    """Bracket every GEMM over the m x n matrix of the pipelines with HIP events."""
     check(lib().bsq_kernel_timer_start(), "kernel timer start")
 
 
 def kernel_timer_stop() -> tuple[float, int]:
-    """Stop bracketing; returns (summed kernel ms, launches) since the start."""
+    """Stop bracketing; returns (summed ms, launches) of the reconstruction GEMMs since the start."""
     ms, n = C.c_double(), C.c_int()
     check(lib().bsq_kernel_timer_stop(C.byref(ms), C.byref(n)), "kernel timer stop")
+    return ms.value, n.value
+
+
+def kernel_timer_read(timer_class: int) -> tuple[float, int]:
+    """After kernel_timer_stop: (summed ms, launches) of one class (TIMER_*)."""
+    ms, n = C.c_double(), C.c_int()
+    check(lib().bsq_kernel_timer_read(timer_class, C.byref(ms), C.byref(n)), "kernel timer read")
     return ms.value, n.value
 
 

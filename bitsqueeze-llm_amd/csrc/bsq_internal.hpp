@@ -167,4 +167,23 @@ void launch_gaussian_fill(float *out, uint64_t n, uint64_t seed, hipStream_t str
 
 int cu_count();
 
+// Instrumentation (off unless started through the ABI): HIP events bracket
+// every GEMM over the m x n matrix inside the pipelines, on the stream it runs
+// on.  Class 0: the low-rank reconstruction; class 1: the range finder's
+// products A_w B and A_w^T B (with their split-K reductions).
+enum GemmTimerClass { kTimeReconstruct = 0, kTimeRangeFinder = 1, kTimeClasses = 2 };
+bool gemm_timer_on();
+void gemm_timer_begin(int cls, hipStream_t stream);
+void gemm_timer_end(int cls, hipStream_t stream);
+template <class F>
+void timed_gemm(int cls, hipStream_t stream, F &&launch) {
+    if (!gemm_timer_on()) {
+        launch();
+        return;
+    }
+    gemm_timer_begin(cls, stream);
+    launch();
+    gemm_timer_end(cls, stream);
+}
+
 }  // namespace bsq

@@ -196,19 +196,15 @@ __global__ void copy_f32x4_kernel(const float4 *__restrict__ src, float4 *__rest
         dst[i] = src[i];
 }
 
-// Optional HIP-event bracketing of the reconstruction GEMM launches inside the
-// compress / decompress pipelines (off unless bsq_kernel_timer_start is
-// called): measures that kernel live, on the stream it runs on.
+// HIP-event bracketing of the GEMMs over the m x n matrix (gemm_timer_*,
+// declared in bsq_internal.hpp): one event pair per timed launch, created on
+// first use and reused afterwards.
 struct KernelTimer {
-    bool on = false;
     std::vector<hipEvent_t> ev;  // pairs: ev[2i] before, ev[2i+1] after
     size_t used = 0;             // pairs recorded since the last read
-    template <class F>
-    void run(hipStream_t st, F &&launch) {
-        if (!on) {
-            launch();
-            return;
-        }
+    double last_ms = 0.0;        // totals of the last read
+    int last_launches = 0;
+    void begin(hipStream_t st) {
         if (2 * used + 2 > ev.size()) {
             hipEvent_t a = nullptr, b = nullptr;
             BSQ_HIP(hipEventCreate(&a));
@@ -220,11 +216,12 @@ struct KernelTimer {
             ev.push_back(b);
         }
         BSQ_HIP(hipEventRecord(ev[2 * used], st));
-        launch();
+    }
+    void end(hipStream_t st) {
         BSQ_HIP(hipEventRecord(ev[2 * used + 1], st));
         ++used;
     }
-    void read(double *total_ms, int *launches) {
+    void read() {
         double t = 0.0;
         for (size_t i = 0; i < used; ++i) {
             BSQ_HIP(hipEventSynchronize(ev[2 * i + 1]));
@@ -232,12 +229,21 @@ struct KernelTimer {
             BSQ_HIP(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
             t += ms;
         }
-        *total_ms = t;
-        *launches = static_cast<int>(used);
+        last_ms = t;
+        last_launches = static_cast<int>(used);
         used = 0;
     }
 };
-KernelTimer g_recon_timer;
+bool g_timer_on = false;
+KernelTimer g_gemm_timer[kTimeClasses];
+
+}  // namespace
+
+bool gemm_timer_on() { return g_timer_on; }
+void gemm_timer_begin(int cls, hipStream_t stream) { g_gemm_timer[cls].begin(stream); }
+void gemm_timer_end(int cls, hipStream_t stream) { g_gemm_timer[cls].end(stream); }
+
+namespace {
 
 bool ratio_is_valid(float r) { return std::isfinite(r) && r >= 0.0f && r <= 1.0f; }
 bool method_is_valid(int m) { return m == kMethodNone || m == kMethodNF4 || m == kMethodNF4DQ; }
@@ -469,7 +475,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
         BSQ_HIP(hipEventRecord(rt.ev[4], st));
         if (te.capacity > 0) {
             // reconstruct + subtract fused (src/bitsqz_llm.cu:1141-1163)
-            g_recon_timer.run(st, [&] {
+            timed_gemm(kTimeReconstruct, st, [&] {
                 launch_reconstruct(U.dense, S.dense, V.dense, rows, cols, rt.q, residual, rt.d_err, st);
             });
             BSQ_HIP(hipEventRecord(rt.ev[5], st));
@@ -599,7 +605,8 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
                 dense[i] = sc.dense;
             }
         }
-        g_recon_timer.run(st, [&] { launch_reconstruct(dense[0], dense[1], dense[2], rows, cols, q, nullptr, d_dst, st); });
+        timed_gemm(kTimeReconstruct, st,
+                   [&] { launch_reconstruct(dense[0], dense[1], dense[2], rows, cols, q, nullptr, d_dst, st); });
     } else {
         const uint64_t N = static_cast<uint64_t>(rows) * cols;
         if (P.d_dense[SEC_DIRECT]) {
@@ -1427,16 +1434,27 @@ int bsq_copy_kernel(const void *d_src, void *d_dst, uint64_t bytes, void *stream
 
 int bsq_kernel_timer_start(void) {
     return guarded([&] {
-        g_recon_timer.on = true;
-        g_recon_timer.used = 0;
+        g_timer_on = true;
+        for (auto &t : g_gemm_timer) t.used = 0;
     });
 }
 
 int bsq_kernel_timer_stop(double *total_ms, int *launches) {
     return guarded([&] {
         BSQ_REQUIRE(total_ms && launches, "null output");
-        g_recon_timer.on = false;
-        g_recon_timer.read(total_ms, launches);
+        g_timer_on = false;
+        for (auto &t : g_gemm_timer) t.read();
+        *total_ms = g_gemm_timer[kTimeReconstruct].last_ms;
+        *launches = g_gemm_timer[kTimeReconstruct].last_launches;
+    });
+}
+
+int bsq_kernel_timer_read(int timer_class, double *total_ms, int *launches) {
+    return guarded([&] {
+        BSQ_REQUIRE(total_ms && launches, "null output");
+        BSQ_REQUIRE(timer_class >= 0 && timer_class < kTimeClasses, "unknown timer class");
+        *total_ms = g_gemm_timer[timer_class].last_ms;
+        *launches = g_gemm_timer[timer_class].last_launches;
     });
 }
 

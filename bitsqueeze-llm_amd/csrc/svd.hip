@@ -349,17 +349,21 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
     }
     // X (Mw x k) = A_w * B (B is Nw x k)
     auto aw_times = [&](const float *Bm, float *out) {
-        if (!p->transposed) launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
-                                        p->gemm_ws_bytes, st);
-        else launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws, p->gemm_ws_bytes,
-                         st);
+        timed_gemm(kTimeRangeFinder, st, [&] {
+            if (!p->transposed) launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
+                                            p->gemm_ws_bytes, st);
+            else launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
+                             p->gemm_ws_bytes, st);
+        });
     };
     // Y (Nw x k) = A_w^T * B (B is Mw x k)
     auto awt_times = [&](const float *Bm, float *out) {
-        if (!p->transposed) launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
-                                        p->gemm_ws_bytes, st);
-        else launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws, p->gemm_ws_bytes,
-                         st);
+        timed_gemm(kTimeRangeFinder, st, [&] {
+            if (!p->transposed) launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
+                                            p->gemm_ws_bytes, st);
+            else launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
+                             p->gemm_ws_bytes, st);
+        });
     };
     // one CholeskyQR pass: out = in * L^{-T}, G = in^T in = L L^T
     auto orth = [&](const float *in, float *out, int rows) {

@@ -124,6 +124,39 @@ __device__ __forceinline__ unsigned long long composite_key(float v, uint32_t c)
     return (static_cast<unsigned long long>(order_key(v)) << 16) | (0xFFFFu - c);
 }
 
+// Number of the n keys in `buf` (LDS, 16-byte aligned) greater than `mine`:
+// 16-byte reads, several in flight, so the loop runs at LDS throughput
+// rather than one read latency per key.
+__device__ __forceinline__ uint32_t count_greater(const unsigned long long *buf, uint32_t n,
+                                                  unsigned long long mine) {
+    const ulonglong2 *b2 = reinterpret_cast<const ulonglong2 *>(buf);
+    uint32_t c0 = 0, c1 = 0;
+#pragma unroll 8
+    for (uint32_t j = 0; j < n / 2; ++j) {
+        const ulonglong2 t = b2[j];
+        c0 += t.x > mine ? 1u : 0u;
+        c1 += t.y > mine ? 1u : 0u;
+    }
+    if (n & 1u) c0 += buf[n - 1] > mine ? 1u : 0u;
+    return c0 + c1;
+}
+
+// Magnitude form of a composite-key threshold K = key(|t|) << 16 | (0xFFFF - c)
+// with key(|t|) >= 1 (a number): |v| reaches key(|t|) exactly when
+// fabsf(v) >= mag (NaN never does), and the composite key of (v, col) is
+// >= K exactly when fabsf(v) > mag, or fabsf(v) == mag and col <= c.
+struct MagThreshold {
+    float mag;
+    uint32_t col;
+    __device__ explicit MagThreshold(unsigned long long K)
+        : mag(__uint_as_float(static_cast<uint32_t>(K >> 16) - 1u)), col(0xFFFFu - static_cast<uint32_t>(K & 0xFFFFu)) {}
+    __device__ bool reaches_key(float v) const { return fabsf(v) >= mag; }
+    __device__ bool reaches(float v, uint32_t c) const {
+        const float x = fabsf(v);
+        return x > mag || (x == mag && c <= col);
+    }
+};
+
 // One radix pass: histogram of digit (K >> shift) & 255 over entries whose
 // already-decided high part equals `prefix`, then choose the digit holding
 // the rank-`remaining` largest entry.  Returns in sh.digit / sh.above.
@@ -268,17 +301,17 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
             // whole waves), so every maximum is compared against the others once
             if (threadIdx.x < ng) {
                 const unsigned long long gmax = tm[threadIdx.x];
-                uint32_t above = 0;
-                const ulonglong2 *tm2 = reinterpret_cast<const ulonglong2 *>(tm);
-                for (uint32_t j = 0; j < ng / 2; ++j) {
-                    const ulonglong2 t2 = tm2[j];
-                    above += (t2.x > gmax ? 1u : 0u) + (t2.y > gmax ? 1u : 0u);
-                }
                 // one group ranks k-1: the maxima of non-empty groups are distinct
-                if (above == k - 1) sh.kt = gmax;
+                if (count_greater(tm, ng, gmax) == k - 1) sh.kt = gmax;
             }
             __syncthreads();
             const unsigned long long kt = sh.kt;
+            // Candidates: the entries whose magnitude reaches the threshold's
+            // (one float compare each): every entry with composite key >= kt,
+            // plus equal magnitudes in later columns, which the exact ranking
+            // below sorts out.  A NaN threshold (key 0) takes the radix path.
+            const bool kt_number = (kt >> 16) != 0;
+            const MagThreshold th(kt_number ? kt : (1ull << 16));
             // count with a bitmask of this lane's hits (<= 64 entries per lane)
             unsigned long long hits = 0;
             uint32_t cnt = 0;
@@ -289,19 +322,18 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
 #pragma unroll 4
                 for (uint32_t c4 = threadIdx.x; c4 < cols / 4; c4 += kThreads, ++i) {
                     const float4 q = cache4[c4];
-                    const uint32_t c = 4 * c4;
-                    const unsigned long long b0 = composite_key(q.x, c) >= kt, b1 = composite_key(q.y, c + 1) >= kt,
-                                             b2 = composite_key(q.z, c + 2) >= kt, b3 = composite_key(q.w, c + 3) >= kt;
+                    const unsigned long long b0 = th.reaches_key(q.x), b1 = th.reaches_key(q.y),
+                                             b2 = th.reaches_key(q.z), b3 = th.reaches_key(q.w);
                     hits |= (b0 | (b1 << 1) | (b2 << 2) | (b3 << 3)) << (4 * i);
                 }
             } else {
                 uint32_t i = 0;
                 for (uint32_t c = threadIdx.x; c < cols; c += kThreads, ++i)
-                    hits |= static_cast<unsigned long long>(composite_key(cache[c], c) >= kt) << i;
+                    hits |= static_cast<unsigned long long>(th.reaches_key(cache[c])) << i;
             }
             cnt = static_cast<uint32_t>(__popcll(hits));
             const uint32_t incl = block_inclusive_scan(cnt, sh.wsum);
-            if (threadIdx.x == kThreads - 1) sh.ncand = incl;
+            if (threadIdx.x == kThreads - 1) sh.ncand = kt_number ? incl : kFastCap + 1;
             __syncthreads();
             const uint32_t total = sh.ncand;
             if (total <= kFastCap) {
@@ -316,8 +348,7 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
                 __syncthreads();
                 for (uint32_t i = threadIdx.x; i < total; i += kThreads) {
                     const unsigned long long mine = buf[i];
-                    uint32_t rank = 0;
-                    for (uint32_t j = 0; j < total; ++j) rank += (buf[j] > mine) ? 1u : 0u;
+                    const uint32_t rank = count_greater(buf, total, mine);
                     if (rank < k) {
                         const uint32_t col = 0xFFFFu - static_cast<uint32_t>(mine & 0xFFFFu);
                         out_idx[rank] = static_cast<uint16_t>(col);
@@ -327,7 +358,8 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
                 }
                 if (a.residual) {
                     __syncthreads();
-                    const unsigned long long kth = sh.kth;
+                    // the k-th largest key is a number here (it reaches kt)
+                    const MagThreshold kth(sh.kth);
                     float *res = a.residual + row0;
                     if ((cols & 3u) == 0 && (reinterpret_cast<uintptr_t>(a.residual) & 15u) == 0) {
                         const float4 *cache4 = reinterpret_cast<const float4 *>(cache);
@@ -335,16 +367,16 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
                         for (uint32_t c4 = threadIdx.x; c4 < cols / 4; c4 += kThreads) {
                             float4 v = cache4[c4];
                             const uint32_t c = 4 * c4;
-                            v.x = (composite_key(v.x, c + 0) >= kth) ? 0.0f : v.x;
-                            v.y = (composite_key(v.y, c + 1) >= kth) ? 0.0f : v.y;
-                            v.z = (composite_key(v.z, c + 2) >= kth) ? 0.0f : v.z;
-                            v.w = (composite_key(v.w, c + 3) >= kth) ? 0.0f : v.w;
+                            v.x = kth.reaches(v.x, c + 0) ? 0.0f : v.x;
+                            v.y = kth.reaches(v.y, c + 1) ? 0.0f : v.y;
+                            v.z = kth.reaches(v.z, c + 2) ? 0.0f : v.z;
+                            v.w = kth.reaches(v.w, c + 3) ? 0.0f : v.w;
                             reinterpret_cast<float4 *>(res)[c4] = v;
                         }
                     } else {
                         for (uint32_t c = threadIdx.x; c < cols; c += kThreads) {
                             const float v = cache[c];
-                            res[c] = (composite_key(v, c) >= kth) ? 0.0f : v;
+                            res[c] = kth.reaches(v, c) ? 0.0f : v;
                         }
                     }
                 }
@@ -478,8 +510,8 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
 template <TopkSource SRC, int NV4>
 __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     __shared__ Shared sh;
-    __shared__ unsigned long long tm[kThreads];
-    __shared__ unsigned long long bk[kFastCap];
+    __shared__ __attribute__((aligned(16))) unsigned long long tm[kThreads];
+    __shared__ __attribute__((aligned(16))) unsigned long long bk[kFastCap];
     __shared__ float bv[kFastCap];
     const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
     const uint32_t r = blockIdx.x, tid = threadIdx.x;
@@ -537,6 +569,12 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     auto lane_id = [&]() -> uint32_t {
         uint32_t t = threadIdx.x;
         asm volatile("" : "+v"(t));
+        // the row values too: keys derived from them in one phase are
+        // recomputed in the next instead of being kept live across it
+#pragma unroll
+        for (int m = 0; m < NV4; ++m)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(v[m][u]));
         return t;
     };
     bool nonzero = false;
@@ -557,23 +595,27 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     }
     tm[tid] = tmax;
     __syncthreads();
-    uint32_t above = 0;
-    for (uint32_t j = 0; j < kThreads; ++j) above += (tm[j] > tmax) ? 1u : 0u;
-    if (above == k - 1) sh.kt = tmax;  // lanes with columns have distinct maxima; k <= those lanes
+    // lanes with columns have distinct maxima; k <= those lanes
+    if (count_greater(tm, kThreads, tmax) == k - 1) sh.kt = tmax;
     __syncthreads();
     unsigned long long kt = sh.kt;
+    // candidates by magnitude (a superset of the keys >= kt, ranked exactly
+    // below); a NaN threshold takes the radix path
+    const bool kt_number = (kt >> 16) != 0;
+    const MagThreshold th(kt_number ? kt : (1ull << 16));
     uint32_t cnt = 0;
     lt = lane_id();
 #pragma unroll
     for (int m = 0; m < NV4; ++m) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) cnt += (key_of(lt, m, u) >= kt) ? 1u : 0u;
+        for (int u = 0; u < 4; ++u) cnt += th.reaches_key(v[m][u]) ? 1u : 0u;
         __builtin_amdgcn_sched_barrier(0);
     }
     uint32_t incl = block_inclusive_scan(cnt, sh.wsum);
-    if (tid == kThreads - 1) sh.ncand = incl;
+    if (tid == kThreads - 1) sh.ncand = kt_number ? incl : kFastCap + 1;
     __syncthreads();
     uint32_t total = sh.ncand;
+    bool exact = false;  // candidates are exactly the keys >= kt (radix path)
     if (total > kFastCap) {
         // fallback: exact threshold by radix select over the registers, on the
         // 32-bit key, then on the inverted column among equal keys
@@ -628,8 +670,9 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         }
         incl = block_inclusive_scan(cnt, sh.wsum);
         total = k;
+        exact = true;
     }
-    // collect the entries at or above kt with their values, then rank them
+    // collect the candidates with their values, then rank them
     uint32_t pos = incl - cnt;
     lt = lane_id();
 #pragma unroll
@@ -637,7 +680,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const unsigned long long K = key_of(lt, m, u);
-            if (K >= kt) {
+            if (exact ? (K >= kt) : th.reaches_key(v[m][u])) {
                 bk[pos] = K;
                 bv[pos] = v[m][u];
                 ++pos;
@@ -650,8 +693,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     float *out_val = a.values + static_cast<uint64_t>(r) * k;
     for (uint32_t i = tid; i < total; i += kThreads) {
         const unsigned long long mine = bk[i];
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < total; ++j) rank += (bk[j] > mine) ? 1u : 0u;
+        const uint32_t rank = count_greater(bk, total, mine);
         if (rank < k) {
             out_idx[rank] = static_cast<uint16_t>(0xFFFFu - static_cast<uint32_t>(mine & 0xFFFFu));
             out_val[rank] = bv[i];
@@ -663,18 +705,36 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         const unsigned long long kth = sh.kth;
         float4 *res4 = reinterpret_cast<float4 *>(a.residual + row0);
         lt = lane_id();
+        if ((kth >> 16) != 0) {  // uniform: the k-th largest is a number
+            const MagThreshold mk(kth);
 #pragma unroll
-        for (int m = 0; m < NV4; ++m) {
-            const uint32_t c4 = lt + kThreads * m;
-            if (c4 < q4) {
-                float4 o;
-                o.x = (key_of(lt, m, 0) >= kth) ? 0.0f : v[m][0];
-                o.y = (key_of(lt, m, 1) >= kth) ? 0.0f : v[m][1];
-                o.z = (key_of(lt, m, 2) >= kth) ? 0.0f : v[m][2];
-                o.w = (key_of(lt, m, 3) >= kth) ? 0.0f : v[m][3];
-                res4[c4] = o;
+            for (int m = 0; m < NV4; ++m) {
+                const uint32_t c4 = lt + kThreads * m;
+                if (c4 < q4) {
+                    const uint32_t c = 4 * c4;
+                    float4 o;
+                    o.x = mk.reaches(v[m][0], c + 0) ? 0.0f : v[m][0];
+                    o.y = mk.reaches(v[m][1], c + 1) ? 0.0f : v[m][1];
+                    o.z = mk.reaches(v[m][2], c + 2) ? 0.0f : v[m][2];
+                    o.w = mk.reaches(v[m][3], c + 3) ? 0.0f : v[m][3];
+                    res4[c4] = o;
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
+        } else {
+#pragma unroll
+            for (int m = 0; m < NV4; ++m) {
+                const uint32_t c4 = lt + kThreads * m;
+                if (c4 < q4) {
+                    float4 o;
+                    o.x = (key_of(lt, m, 0) >= kth) ? 0.0f : v[m][0];
+                    o.y = (key_of(lt, m, 1) >= kth) ? 0.0f : v[m][1];
+                    o.z = (key_of(lt, m, 2) >= kth) ? 0.0f : v[m][2];
+                    o.w = (key_of(lt, m, 3) >= kth) ? 0.0f : v[m][3];
+                    res4[c4] = o;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 }
@@ -832,11 +892,14 @@ bool try_launch_reg(const TopkArgs &a, hipStream_t stream) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(a.a) | reinterpret_cast<uintptr_t>(a.residual) |
                          (SRC == TopkSource::DenseMinusDense ? reinterpret_cast<uintptr_t>(a.b) : 0);
     if ((a.cols & 3u) != 0 || (al & 15u) != 0 || a.k > kThreads || a.k > a.cols / 4) return false;
-    // longer rows need more than 128 VGPRs per lane here, which halves the
-    // resident rows; the LDS-cached kernel serves them better
+    // rows up to 11264 columns (44 values per lane, about 120 VGPRs: four
+    // rows per CU, one more than the LDS-cached kernel fits); longer rows
+    // would pass 128 VGPRs and halve the resident rows
     const uint32_t nv4 = static_cast<uint32_t>(ceil_div(a.cols / 4, kThreads));
     if (nv4 <= 2) launch_reg<SRC, 2>(a, stream);
     else if (nv4 <= 4) launch_reg<SRC, 4>(a, stream);
+    else if (nv4 <= 8) launch_reg<SRC, 8>(a, stream);
+    else if (nv4 <= 11) launch_reg<SRC, 11>(a, stream);
     else return false;
     return true;
 }

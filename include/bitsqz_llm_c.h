@@ -243,10 +243,13 @@ BSQ_API int bsq_event_record(void *event, void *stream);
 BSQ_API int bsq_event_elapsed_ms(void *start, void *stop, float *ms);
 
 /* Instrumentation (no counterpart in the reference): while started, every
- * low-rank reconstruction GEMM launched by the compress / decompress
- * pipelines is bracketed by HIP events on its own stream.  _stop waits for
- * those events and returns the summed kernel time and the launch count. */
+ * GEMM over the m x n matrix launched by the compress / decompress pipelines
+ * is bracketed by HIP events on its own stream.  _stop waits for those events
+ * and returns the summed time and launch count of the low-rank reconstruction
+ * GEMMs; _read then returns either class: 0 = reconstruction, 1 = the range
+ * finder's products with the big matrix (split-K reductions included). */
 BSQ_API int bsq_kernel_timer_start(void);
+BSQ_API int bsq_kernel_timer_read(int timer_class, double *total_ms, int *launches);
 /* Plain device copy kernel (16 bytes per lane), the known-size reference for
  * calibrating HBM byte counters.  bytes and both pointers 16-byte aligned. */
 BSQ_API int bsq_copy_kernel(const void *d_src, void *d_dst, uint64_t bytes, void *stream);

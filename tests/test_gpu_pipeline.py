@@ -52,6 +52,9 @@ CASES = [
     ("fp32_direct_plain", 64, 64, 0.0, 0.3, B.QUANT_NONE, B.INPUT_DEVICE),
     ("odd_shape_nf4_error", 37, 101, 0.03, 0.07, B.NF4, B.INPUT_DEVICE),
     ("odd_shape_nf4dq_error", 33, 99, 0.0, 0.5, B.NF4_DQ, B.INPUT_HOST),
+    # the headline width: 11 column quads per lane in the register top-k
+    ("wide_nf4dq_outlier_error", 128, 11008, 0.005, 0.01, B.NF4_DQ, B.INPUT_DEVICE),
+    ("wide_nf4_error", 64, 11008, 0.0, 0.01, B.NF4, B.INPUT_DEVICE),
 ]
 
 

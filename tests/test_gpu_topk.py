@@ -66,6 +66,34 @@ def test_ties_nan_inf_zero_rows():
         _check(x, k)
 
 
+@pytest.mark.parametrize("cols", [600, 4096, 8000, 11008, 14336, 20000])
+def test_ties_at_threshold_every_kernel(cols):
+    """Heavy ties in magnitude (integers -3..3 and their negatives, so equal
+    |v| sits on both sides of the k-th entry), NaN / inf / +-0 / subnormal
+    rows, at widths served by each kernel variant (register rows of 2, 4, 8
+    and 11 quads, the LDS-cached and the uncached kernel); the separation
+    residual zeroes exactly the selected entries."""
+    rng = np.random.default_rng(cols)
+    x = rng.integers(-3, 4, (12, cols)).astype(np.float32)
+    x[0] = 0.0
+    x[1] = np.nan
+    x[2, ::3] = np.nan
+    x[3, 5] = np.inf
+    x[3, 9] = -np.inf
+    x[4] = -0.0
+    x[5, : cols // 2] = 1e-42
+    x[6] = rng.standard_normal(cols).astype(np.float32)
+    x[7, ::2] = np.nan
+    x[7, 1::2] = 2.0
+    for k in (1, 64, 256):
+        idx, val, res = B.topk_select(x, k, separate=True)
+        ei, ev = O.topk_rows(x, k)
+        assert idx.tobytes() == ei.tobytes() and val.tobytes() == ev.tobytes()
+        expect = x.copy()
+        np.put_along_axis(expect, ei.astype(np.int64), 0.0, axis=1)
+        assert res.tobytes() == expect.tobytes()
+
+
 def test_outlier_columns_like_config2():
     rng = np.random.default_rng(0)
     x = rng.standard_normal((512, 4096)).astype(np.float32)
