@@ -167,6 +167,17 @@ void launch_gaussian_fill(float *out, uint64_t n, uint64_t seed, hipStream_t str
 
 int cu_count();
 
+// Reconstruction from NF4 / NF4_DQ factors decoded inline (recon.hip): U
+// (m x k) and V (n x k) are packed nibbles with their block scales (and the
+// device dq of NF4_DQ), S is FP32; out = U diag(S) V^T, bit for bit what
+// decoding the factors and launch_reconstruct give.  Supported for
+// k % 64 == 0, 64 <= k <= kReconQMaxK and 16-byte aligned code arrays.
+constexpr int kReconQMaxK = 512;
+bool recon_q_supported(int m, int n, int k, const uint8_t *u_codes, const uint8_t *v_codes);
+void launch_recon_q(int method, const uint8_t *u_codes, const float *u_scales_f32, const uint8_t *u_scales_u8,
+                    const float *u_dq, const uint8_t *v_codes, const float *v_scales_f32, const uint8_t *v_scales_u8,
+                    const float *v_dq, const float *S, int m, int n, int k, float *out, hipStream_t stream);
+
 // Instrumentation (off unless started through the ABI): HIP events bracket
 // every GEMM over the m x n matrix inside the pipelines, on the stream it runs
 // on.  Class 0: the low-rank reconstruction; class 1: the range finder's

@@ -26,6 +26,7 @@
 // along K so the grid fills the 256 CUs several times over; partial products
 // go to a workspace summed in a fixed order, so results are deterministic.
 #include "bsq_internal.hpp"
+#include "tile_map.hpp"
 
 namespace bsq {
 namespace {
@@ -44,7 +45,8 @@ struct GemmArgs {
     const float *minuend;     // optional: C = minuend - acc (ldc layout)
     int M, N, K;
     int lda, ldb, ldc;
-    int k_per_split;          // K range of one blockIdx.z (multiple of BK)
+    int k_per_split;          // K range of one split (multiple of BK)
+    int splits;               // K ranges, i.e. work items per output tile
     uint64_t split_stride;    // elements between split-K partial outputs
     bool vec_a, vec_b;        // 16-byte loads allowed (alignment of base and leading dim)
 };
@@ -163,27 +165,6 @@ struct KMajor {
     }
 };
 
-// Tile of workgroup `bid` (1-D grid over the ny x nx output tiles).  The
-// hardware deals workgroups to the 8 XCDs round-robin (bid % 8), and each
-// XCD has its own L2: give XCD x a contiguous range of logical tiles, and
-// walk the logical order in groups of kGroupRows tile rows with the column
-// index outermost, so the workgroups resident on one XCD share a few A
-// panels and a few B panels instead of touching every panel of both
-// operands (which re-fetches them from HBM).  A bijection onto the tiles for
-// any grid size.
-constexpr int kXcds = 8, kGroupRows = 8;
-__device__ __forceinline__ void xcd_tile(int bid, int ny, int nx, int &tm, int &tn) {
-    const int T = ny * nx;
-    const int xcd = bid % kXcds, loc = bid / kXcds;
-    const int per = T / kXcds, rem = T % kXcds;
-    const int L = xcd * per + min(xcd, rem) + loc;
-    const int span = kGroupRows * nx;
-    const int first = (L / span) * kGroupRows;
-    const int rows = min(ny - first, kGroupRows);
-    const int in = L % span;
-    tm = first + in % rows;
-    tn = in / rows;
-}
 
 // RECON: the low-rank reconstruction form (column scale on op(A), optional
 // minuend), instantiated separately so the power-iteration GEMMs carry no
@@ -205,10 +186,10 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
-    int tile_m, tile_n;
-    xcd_tile(blockIdx.x, ceil_div(g.M, BM), ceil_div(g.N, BN), tile_m, tile_n);
+    int tile_m, tile_n, zs;
+    xcd_tile(ceil_div(g.M, BM), ceil_div(g.N, BN), g.splits, tile_m, tile_n, zs);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
-    const int kbeg = blockIdx.z * g.k_per_split;
+    const int kbeg = zs * g.k_per_split;
     const int kend = min(g.K, kbeg + g.k_per_split);
 
     f32x4v acc[FM][FN];
@@ -278,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g) {
     }
 
     // epilogue: fragment (i, j) register r holds row 4*(lane/16) + r, column lane % 16
-    float *C = g.C + static_cast<uint64_t>(blockIdx.z) * g.split_stride;
+    float *C = g.C + static_cast<uint64_t>(zs) * g.split_stride;
     if constexpr (RECON) {
         // the reconstruction writes (and may subtract from) a full m x n matrix:
         // stage the tile through LDS (the operand buffers are free now) in two
@@ -448,10 +429,10 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
-    int tile_m, tile_n;
-    xcd_tile(blockIdx.x, ceil_div(g.M, BM), ceil_div(g.N, BN), tile_m, tile_n);
+    int tile_m, tile_n, zs;
+    xcd_tile(ceil_div(g.M, BM), ceil_div(g.N, BN), g.splits, tile_m, tile_n, zs);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
-    const int kbeg = blockIdx.z * g.k_per_split;
+    const int kbeg = zs * g.k_per_split;
     const int kend = min(g.K, kbeg + g.k_per_split);
     const int nk = (kend - kbeg) / BK;
 
@@ -485,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
     constexpr int kMv = RECON ? 4 * Q : 0;
     float4 mvall[4][Q];
     const bool vec_c = RECON && ((g.ldc & 3) == 0) &&
-                       ((reinterpret_cast<uintptr_t>(g.C + static_cast<uint64_t>(blockIdx.z) * g.split_stride) & 15u) == 0) &&
+                       ((reinterpret_cast<uintptr_t>(g.C + static_cast<uint64_t>(zs) * g.split_stride) & 15u) == 0) &&
                        (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
     const bool mv_on = RECON && g.minuend && vec_c && g.N >= 4;
     auto issue_minuend = [&]() {
@@ -549,7 +530,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
         if (j + 3 < nk) body(st3, st2, j + 3);
     }
 
-    float *C = g.C + static_cast<uint64_t>(blockIdx.z) * g.split_stride;
+    float *C = g.C + static_cast<uint64_t>(zs) * g.split_stride;
     // fragment (i, j) register r holds row 4*(lane/16) + r, column lane % 16
     if constexpr (RECON) {
         // the output tile leaves through stage 0 in four 32-row passes so that
@@ -693,7 +674,8 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
         g.ldc = ldc;
         g.split_stride = 0;
     }
-    dim3 grid(static_cast<unsigned>(ceil_div(N, BN) * ceil_div(M, BM)), 1, splits);
+    g.splits = splits;
+    dim3 grid(static_cast<unsigned>(ceil_div(N, BN) * ceil_div(M, BM) * splits));
     const bool recon = a_colscale || minuend;
     // the DMA-pipelined kernel wherever its layout constraints hold, else the
     // register-staged one
@@ -704,7 +686,7 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
     const bool t64 = dma && !recon && splits == 1 &&
                      ceil_div(M, BM) * ceil_div(N, BN) < 2 * static_cast<uint64_t>(cu_count());
     if (t64) {
-        grid.x = static_cast<unsigned>(ceil_div(N, 64) * ceil_div(M, 64));
+        grid.x = static_cast<unsigned>(ceil_div(N, 64) * ceil_div(M, 64));  // unsplit
         if (!ta && !tb) gemm_dma_kernel<false, false, false, 64><<<grid, kThreads, 0, stream>>>(g);
         else if (ta && !tb) gemm_dma_kernel<true, false, false, 64><<<grid, kThreads, 0, stream>>>(g);
         else if (!ta && tb) gemm_dma_kernel<false, true, false, 64><<<grid, kThreads, 0, stream>>>(g);

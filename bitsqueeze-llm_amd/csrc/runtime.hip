@@ -591,22 +591,37 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
                        hipStream_t st, const uint32_t *err_gate = nullptr, bool scatter = true) {
     const bitsqz_llm_array_t &H = P.header;
     const uint32_t rows = H.num_rows, cols = H.num_columns;
+    const bool has_outlier = (H.flags & kFlagOutlier) != 0;
+    const uint32_t ke = has_error ? P.topk_k[1] : 0, ko = has_outlier ? P.topk_k[0] : 0;
     if (H.flags & kFlagSvd) {
         const int q = static_cast<uint16_t>(H.effective_rank);
+        // packed U and V: the reconstruction decodes them inline
+        const bool fused = H.svd_uv_format != kMethodNone && !P.d_dense[SEC_U] && !P.d_dense[SEC_V] &&
+                           recon_q_supported(rows, cols, q, P.d_codes[SEC_U], P.d_codes[SEC_V]);
         const float *dense[3];
         for (int i = 0; i < 3; ++i) {
             if (P.d_dense[i]) {
                 dense[i] = P.d_dense[i];
-            } else {
+            } else if (!(fused && i != SEC_S)) {
                 Section &sc = rt.sec[i];  // decompress runtime's dense U / S / V
                 const int method = (i == SEC_S) ? H.svd_s_format : H.svd_uv_format;
                 launch_quant_decode(P.count[i], method, P.d_scales_f32[i], P.d_scales_u8[i], P.d_dq_scale[i],
                                     P.d_codes[i], sc.dense, st);
                 dense[i] = sc.dense;
+            } else {
+                dense[i] = nullptr;
             }
         }
-        timed_gemm(kTimeReconstruct, st,
-                   [&] { launch_reconstruct(dense[0], dense[1], dense[2], rows, cols, q, nullptr, d_dst, st); });
+        if (fused) {
+            timed_gemm(kTimeReconstruct, st, [&] {
+                launch_recon_q(H.svd_uv_format, P.d_codes[SEC_U], P.d_scales_f32[SEC_U], P.d_scales_u8[SEC_U],
+                               P.d_dq_scale[SEC_U], P.d_codes[SEC_V], P.d_scales_f32[SEC_V], P.d_scales_u8[SEC_V],
+                               P.d_dq_scale[SEC_V], dense[SEC_S], rows, cols, q, d_dst, st);
+            });
+        } else {
+            timed_gemm(kTimeReconstruct, st,
+                       [&] { launch_reconstruct(dense[0], dense[1], dense[2], rows, cols, q, nullptr, d_dst, st); });
+        }
     } else {
         const uint64_t N = static_cast<uint64_t>(rows) * cols;
         if (P.d_dense[SEC_DIRECT]) {
@@ -617,9 +632,8 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
         }
     }
     if (!scatter) return;
-    const bool has_outlier = (H.flags & kFlagOutlier) != 0;
-    launch_topk_scatter(P.d_topk_idx[1], P.d_topk_val[1], has_error ? P.topk_k[1] : 0, P.d_topk_idx[0],
-                        P.d_topk_val[0], has_outlier ? P.topk_k[0] : 0, rows, cols, d_dst, true, st, err_gate);
+    launch_topk_scatter(P.d_topk_idx[1], P.d_topk_val[1], ke, P.d_topk_idx[0], P.d_topk_val[0], ko, rows, cols, d_dst,
+                        true, st, err_gate);
 }
 
 // True when some index of the host top-k blob at `p` (num_topk_columns per
@@ -929,6 +943,24 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         P.topk_k[t] = h.num_topk_columns;
     }
 
+    // Packed U and V of the SVD path stay packed for the reconstruction, which
+    // decodes them inline, when both fit the shared staging side by side;
+    // otherwise every section is decoded as soon as it arrives (the staging
+    // is then shared).
+    const uint64_t uq = (c->flags & kFlagSvd) ? static_cast<uint64_t>(rows) * static_cast<uint16_t>(c->effective_rank) : 0;
+    const uint64_t vq = (c->flags & kFlagSvd) ? static_cast<uint64_t>(cols) * static_cast<uint16_t>(c->effective_rank) : 0;
+    const uint64_t v_code_off = ceil_div(uq / 2, 256) * 256, v_scale_off = ceil_div(uq / kQuantBlock, 64) * 64;
+    // a packed S is decoded at once, from behind V (U and V must stay intact)
+    const uint64_t s_code_off = ceil_div(v_code_off + vq / 2, 256) * 256,
+                   s_scale_off = ceil_div(v_scale_off + vq / kQuantBlock, 64) * 64;
+    const uint64_t sq = (c->flags & kFlagSvd) ? static_cast<uint16_t>(c->effective_rank) : 0;
+    const bool keep_packed = (c->flags & kFlagSvd) && c->svd_uv_format != kMethodNone && rt.quant_initialized &&
+                             c->section_u.storage == BITSQZ_SECTION_QUANT &&
+                             c->section_v.storage == BITSQZ_SECTION_QUANT &&
+                             recon_q_supported(rows, cols, static_cast<uint16_t>(c->effective_rank), rt.q_codes,
+                                               rt.q_codes + v_code_off) &&
+                             s_code_off + (sq + 1) / 2 <= (N + 1) / 2 &&
+                             s_scale_off + ceil_div(sq, kQuantBlock) <= ceil_div(N, kQuantBlock);
     auto stage_section = [&](int i, const bitsqz_section_t &s, int method, uint64_t count, float *dense_dst) {
         if (s.storage == BITSQZ_SECTION_FP32) {
             BSQ_REQUIRE(s.size == count * 4, "FP32 section size mismatch");
@@ -945,16 +977,29 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         const uint8_t *pl = staged(s);
         const uint64_t nb = h.num_blocks;
         const uint64_t ssz = method == kMethodNF4 ? nb * 4 : nb;
-        void *sdst = method == kMethodNF4 ? static_cast<void *>(rt.q_scales_f32) : static_cast<void *>(rt.q_scales_u8);
+        // packed U at the start of the staging, packed V after it
+        const bool packed = keep_packed && (i == SEC_U || i == SEC_V);
+        const uint64_t coff = !keep_packed ? 0 : (i == SEC_V ? v_code_off : (i == SEC_S ? s_code_off : 0));
+        const uint64_t soff = !keep_packed ? 0 : (i == SEC_V ? v_scale_off : (i == SEC_S ? s_scale_off : 0));
+        float *sc_f32 = rt.q_scales_f32 + soff;
+        uint8_t *sc_u8 = rt.q_scales_u8 + soff, *codes = rt.q_codes + coff;
+        void *sdst = method == kMethodNF4 ? static_cast<void *>(sc_f32) : static_cast<void *>(sc_u8);
         BSQ_HIP(hipMemcpyAsync(sdst, pl + s.offset + 48, ssz, hipMemcpyHostToDevice, st));
-        BSQ_HIP(hipMemcpyAsync(rt.q_codes, pl + s.offset + 48 + ssz, (count + 1) / 2, hipMemcpyHostToDevice, st));
+        BSQ_HIP(hipMemcpyAsync(codes, pl + s.offset + 48 + ssz, (count + 1) / 2, hipMemcpyHostToDevice, st));
         if (method == kMethodNF4DQ)
             BSQ_HIP(hipMemcpyAsync(&rt.meta->dq[i], pl + s.offset + 40, 4, hipMemcpyHostToDevice, st));
-        // decode now (the staging buffers are shared between sections)
-        launch_quant_decode(count, method, rt.q_scales_f32, rt.q_scales_u8, &rt.meta->dq[i], rt.q_codes, dense_dst,
-                            st);
-        P.d_dense[i] = dense_dst;
         P.count[i] = count;
+        if (packed) {
+            P.d_dense[i] = nullptr;
+            P.d_codes[i] = codes;
+            P.d_scales_f32[i] = method == kMethodNF4 ? sc_f32 : nullptr;
+            P.d_scales_u8[i] = method == kMethodNF4DQ ? sc_u8 : nullptr;
+            P.d_dq_scale[i] = method == kMethodNF4DQ ? &rt.meta->dq[i] : nullptr;
+            return;
+        }
+        // decode now (the staging buffers are shared between sections)
+        launch_quant_decode(count, method, sc_f32, sc_u8, &rt.meta->dq[i], codes, dense_dst, st);
+        P.d_dense[i] = dense_dst;
     };
     if (c->flags & kFlagSvd) {
         const uint16_t q = static_cast<uint16_t>(c->effective_rank);
