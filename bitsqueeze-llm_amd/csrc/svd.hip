@@ -39,6 +39,8 @@ void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *st
                          const int *run = nullptr);
 void launch_orth_refine(const double *G, const double *rowsq, int k, double *Lbuf, float *B, int *status, int *run,
                         hipStream_t stream);
+void launch_chol_solve(const double *G, int k, double *Lbuf, const float *X, int M, float *Q, int *status,
+                       hipStream_t stream);
 void launch_syev(const double *G, int k, double *W, double *Z, double *small, double *scratch, int *iscratch,
                  double *lambda, float *Uh, hipStream_t stream);
 
@@ -368,10 +370,8 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
     // one CholeskyQR pass: out = in * L^{-T}, G = in^T in = L L^T
     auto orth = [&](const float *in, float *out, int rows) {
         launch_gram(in, rows, k, k, p->G, p->gram_ws, st);
-        if (p->Lbuf) {  // Linv holds L^{-T}: out = in * Linv
-            launch_chol_blocked(p->G, k, p->Lbuf, p->Linv, p->status, st);
-            launch_gemm(false, false, rows, k, k, in, k, p->Linv, k, out, k, nullptr, nullptr, p->gemm_ws,
-                        p->gemm_ws_bytes, st);
+        if (p->Lbuf) {  // out L^T = in, by blocked forward substitution
+            launch_chol_solve(p->G, k, p->Lbuf, in, rows, out, p->status, st);
             return;
         }
         launch_chol_inv(p->G, k, p->W, p->Linv, p->status, p->scratch, st);  // Linv holds L^{-1}
