@@ -131,6 +131,15 @@ def lib():
         "bsq_copy_kernel": (i32, [P, P, u64, P]),
         "bsq_kernel_timer_stop": (i32, [C.POINTER(C.c_double), C.POINTER(i32)]),
         "bsq_kernel_timer_read": (i32, [i32, C.POINTER(C.c_double), C.POINTER(i32)]),
+        "bsq_legacy_compress": (i32, [i32, P, u64, C.POINTER(P)]),
+        "bsq_legacy_decompress": (i32, [P, P, u64]),
+        "bsq_legacy_packed_size": (C.c_longlong, [P]),
+        "bsq_legacy_load": (P, [P, C.c_longlong]),
+        "bsq_legacy_free": (None, [P]),
+        "bsq_legacy_payload_bytes": (C.c_longlong, [i32, u64]),
+        "bsq_legacy_encode_device": (i32, [i32, P, u64, P, P]),
+        "bsq_legacy_decode_device": (i32, [i32, P, u64, P, P]),
+        "bsq_legacy_sweep": (i32, [i32, u64, u64, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -487,3 +496,77 @@ def device_synchronize():
 
 def runtime_stream():
     return lib().bsq_runtime_stream()
+
+
+# ---------------------------------------------------------------------------
+# legacy quantisation formats (include/quantization.hpp)
+# ---------------------------------------------------------------------------
+LEGACY_Q8_0, LEGACY_Q4_0, LEGACY_Q2_K, LEGACY_BF16, LEGACY_FP16, LEGACY_FP8, LEGACY_FP4 = 0, 1, 2, 3, 4, 5, 6
+LEGACY_MXFP8, LEGACY_MXFP4, LEGACY_NVFP4, LEGACY_NF4_DQ, LEGACY_NF4, LEGACY_Q2_K_FAST = 7, 8, 9, 10, 11, 12
+
+
+def legacy_compress_handle(method: int, x: np.ndarray):
+    """quantization_compress of host floats; returns (rc, buffer pointer)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = C.c_void_p()
+    rc = lib().bsq_legacy_compress(method, _ptr(x) if x.size else None, x.size, C.byref(out))
+    return rc, out
+
+
+def legacy_compress(method: int, x: np.ndarray) -> bytes:
+    """The serialised buffer (quantization_get_packed_size bytes)."""
+    rc, h = legacy_compress_handle(method, x)
+    check(rc, "quantization_compress")
+    try:
+        size = lib().bsq_legacy_packed_size(h)
+        assert size > 0
+        return C.string_at(h, size)
+    finally:
+        lib().bsq_legacy_free(h)
+
+
+def legacy_decompress(buf: bytes, n: int, dst_n: int | None = None):
+    """load_quantization_from_buffer + quantization_decompress; returns
+    (rc, floats) with rc = -1 when the load is refused."""
+    raw = C.create_string_buffer(buf, len(buf))
+    h = lib().bsq_legacy_load(raw, len(buf))
+    if not h:
+        return -1, None
+    try:
+        out = np.zeros(max(n, 1), np.float32)
+        rc = lib().bsq_legacy_decompress(h, _ptr(out), n if dst_n is None else dst_n)
+        return rc, out[:n]
+    finally:
+        lib().bsq_legacy_free(h)
+
+
+def legacy_payload_bytes(method: int, n: int) -> int:
+    return int(lib().bsq_legacy_payload_bytes(method, n))
+
+
+def legacy_encode_device(method: int, x: np.ndarray) -> bytes:
+    """Payload image written by the device encoder (pointer fields as the
+    device left them)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    size = legacy_payload_bytes(method, x.size)
+    src = DeviceBuffer.from_array(x)
+    img = DeviceBuffer(size)
+    check(lib().bsq_legacy_encode_device(method, src.ptr, x.size, img.ptr, None), "legacy encode")
+    check(lib().bsq_stream_synchronize(None), "sync")
+    return img.download(np.uint8, size).tobytes()
+
+
+def legacy_decode_device(method: int, payload: bytes, n: int) -> np.ndarray:
+    img = DeviceBuffer.from_array(np.frombuffer(payload, np.uint8))
+    dst = DeviceBuffer(4 * n)
+    check(lib().bsq_legacy_decode_device(method, img.ptr, n, dst.ptr, None), "legacy decode")
+    check(lib().bsq_stream_synchronize(None), "sync")
+    return dst.download(np.float32, n)
+
+
+def legacy_sweep(kind: int, lo: int, hi: int) -> int:
+    d = DeviceBuffer(8)
+    d.zero()
+    check(lib().bsq_legacy_sweep(kind, lo, hi, d.ptr, None), "legacy sweep")
+    check(lib().bsq_stream_synchronize(None), "sync")
+    return int(d.download(np.uint64, 1)[0])

@@ -60,6 +60,8 @@ struct Error : std::runtime_error {
 };
 
 [[noreturn]] void fail(const std::string &msg);
+// Sets the message bsq_last_error() returns on this thread ("" clears it).
+void set_last_error(const char *msg);
 void hip_check(hipError_t e, const char *what);
 
 #define BSQ_HIP(call) ::bsq::hip_check((call), #call)

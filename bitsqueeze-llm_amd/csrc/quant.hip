@@ -16,6 +16,7 @@
 // This file is compiled with -ffp-contract=off: every multiply and subtract
 // below must round on its own, as in the reference.
 #include "bsq_internal.hpp"
+#include "scalar_codecs.hpp"
 
 #include <cfloat>
 
@@ -82,42 +83,6 @@ __device__ __forceinline__ uint32_t nf4_code(const Nf4Table &t, float v) {
         return t.lo[b] + ((v >= t.thr[b]) ? 1u : 0u);
     }
     return nf4_code_scan(v);
-}
-
-// FP8 E4M3 encode exactly as quantization_cuda.cu:64-109 writes it.
-__device__ __forceinline__ uint32_t e4m3_encode(float value) {
-    if (!__builtin_isfinite(value)) value = (value < 0.0f) ? -kE4M3Max : kE4M3Max;
-    const uint32_t sign = __builtin_signbit(value) ? 1u : 0u;
-    float a = fabsf(value);
-    if (a == 0.0f) return sign << 7;
-    if (a > kE4M3Max) a = kE4M3Max;
-    int e2 = 0;
-    const float mant = frexpf(a, &e2);
-    int ef = e2 - 1 + 7;
-    if (ef <= 0) {
-        int mf = static_cast<int>(rintf(a * 512.0f));
-        if (mf > 7) mf = 7;
-        return (sign << 7) | static_cast<uint32_t>(mf & 7);
-    }
-    int mf = static_cast<int>(rintf(((mant * 2.0f) - 1.0f) * 8.0f));
-    if (mf > 7) {
-        mf = 0;
-        ef += 1;
-    }
-    if (ef >= 16) {
-        ef = 15;
-        mf = 7;
-    }
-    return (sign << 7) | (static_cast<uint32_t>(ef & 15) << 3) | static_cast<uint32_t>(mf & 7);
-}
-
-// FP8 E4M3 decode (quantization_cuda.cu:111-128); 0x7F decodes to 480.
-__device__ __forceinline__ float e4m3_decode(uint32_t v) {
-    const uint32_t ef = (v >> 3) & 15u, mf = v & 7u;
-    float r;
-    if (ef == 0) r = (static_cast<float>(mf) / 8.0f) * 0.015625f;  // 2^(1-7)
-    else r = (1.0f + static_cast<float>(mf) / 8.0f) * __builtin_ldexpf(1.0f, static_cast<int>(ef) - 7);
-    return (v & 0x80u) ? -r : r;
 }
 
 // max over the aligned group of 8 lanes (quad xor-1, quad xor-2, half-row

@@ -239,6 +239,8 @@ KernelTimer g_gemm_timer[kTimeClasses];
 
 }  // namespace
 
+void set_last_error(const char *msg) { set_error(msg); }
+
 bool gemm_timer_on() { return g_timer_on; }
 void gemm_timer_begin(int cls, hipStream_t stream) { g_gemm_timer[cls].begin(stream); }
 void gemm_timer_end(int cls, hipStream_t stream) { g_gemm_timer[cls].end(stream); }

@@ -255,6 +255,46 @@ BSQ_API int bsq_kernel_timer_read(int timer_class, double *total_ms, int *launch
 BSQ_API int bsq_copy_kernel(const void *d_src, void *d_dst, uint64_t bytes, void *stream);
 BSQ_API int bsq_kernel_timer_stop(double *total_ms, int *launches);
 
+/* ---------------------------------------------------------------------------
+ * 5. Legacy quantisation formats (include/quantization.hpp): the reference's
+ *    CPU codec dispatcher, here encoding and decoding on the GPU.
+ * ------------------------------------------------------------------------- */
+/* extern "C" twins of the five C++-linkage functions of include/quantization.hpp;
+ * replace quantization_compress / quantization_decompress /
+ * quantization_get_packed_size / load_quantization_from_buffer /
+ * quantization_free, reference
+ * legacy_modules/quantization/src/quantization.cpp:125-489.  `method` is a
+ * quantization_method_t value; buffers are quantization_buffer_t *. */
+BSQ_API int bsq_legacy_compress(int method, const float *src, uint64_t n, void **out);
+BSQ_API int bsq_legacy_decompress(const void *buf, float *dst, uint64_t n);
+BSQ_API long long bsq_legacy_packed_size(const void *buf);
+BSQ_API void *bsq_legacy_load(const void *buffer, long long size);
+BSQ_API void bsq_legacy_free(void *buf);
+
+/* Bytes of the payload (format struct + arrays) of n elements, or -1.  The
+ * reference's get_*_array_size (e.g. q8_0_impl.cpp:3-6) on the struct that
+ * its compress writes. */
+BSQ_API long long bsq_legacy_payload_bytes(int method, uint64_t n);
+
+/* Device-resident codec (no reference counterpart: the reference codecs take
+ * host arrays).  Encode writes the payload image of n device floats to
+ * d_payload (16-byte aligned, bsq_legacy_payload_bytes bytes): the format
+ * struct with its counts and scale, then its arrays, byte-identical to the
+ * reference's payload except the struct's pointer fields, which are left
+ * unspecified (FP8, FP4, NVFP4 and NF4_DQ use one as reduction scratch).
+ * Decode reads such an image of n elements.  Asynchronous on `stream`. */
+BSQ_API int bsq_legacy_encode_device(int method, const float *d_src, uint64_t n, void *d_payload,
+                                     void *stream);
+BSQ_API int bsq_legacy_decode_device(int method, const void *d_payload, uint64_t n, float *d_dst,
+                                     void *stream);
+
+/* Test hook: adds to *d_checksum the sum over float patterns p in [lo, hi)
+ * (hi <= 2^32) of (r(p) + 1) * (p mod 65521), where r is the device FP16
+ * conversion (kind 0), BF16 conversion (1) or MX block exponent as a byte
+ * (2: max norm 448, 3: max norm 6). */
+BSQ_API int bsq_legacy_sweep(int kind, uint64_t lo, uint64_t hi, unsigned long long *d_checksum,
+                             void *stream);
+
 #ifdef __cplusplus
 }
 #endif
