@@ -21,6 +21,7 @@ exists.
 
     python bench.py --calibrate-copy   # also launches the plain copy kernel
                                        # (for rocprofv3 --pmc calibration runs)
+    python bench.py --legacy           # the legacy formats' device codecs
 """
 from __future__ import annotations
 
@@ -265,6 +266,139 @@ def cpu_baseline(x, direct, reps=5):
             "one_thread": runs["one"], "nproc": nproc, "cpu_model": model, "sockets": sockets}
 
 
+# The reference's legacy format benches (tests/quantization/test_*_impl.cpp):
+# 5 arrays of 4 194 304 uniform[-10, 10] floats per method.
+LEGACY_ARRAYS, LEGACY_N = 5, 4194304
+LEGACY_NAMES = {0: "Q8_0", 1: "Q4_0", 2: "Q2_K", 3: "BF16", 4: "FP16", 5: "FP8", 6: "FP4", 7: "MXFP8",
+                8: "MXFP4", 9: "NVFP4", 10: "NF4_DQ", 11: "NF4", 12: "Q2_K_FAST"}
+
+
+def legacy_cpu_baseline(x, reps=3):
+    """The reference's legacy dispatcher (quantization.cpp:125-476 and the
+    eleven impl/*.cpp codecs, compiled from its own sources into
+    oracle/_ref/libref_legacy.so) on one array of the workload per method:
+    quantization_compress and quantization_decompress timed separately
+    (1 warmup + mean of `reps`) with every host thread this job may use."""
+    import ctypes
+
+    so = os.path.join(ROOT, "oracle", "_ref", "libref_legacy.so")
+    if not os.path.exists(so):
+        return None
+    L = ctypes.CDLL(so)
+    L.ref_legacy_set_threads.argtypes = [ctypes.c_int]
+    L.ref_legacy_set_threads.restype = ctypes.c_int
+    P = ctypes.c_void_p
+    D = ctypes.POINTER(ctypes.c_double)
+    L.ref_legacy_roundtrip.argtypes = [ctypes.c_int, P, ctypes.c_ulonglong, P, ctypes.c_int, D, D]
+    nproc, model, sockets = host_cpu_info()
+    threads = L.ref_legacy_set_threads(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc)
+    out = np.empty(x.size, np.float32)
+    per, tot = {}, 0.0
+    for m, name in LEGACY_NAMES.items():
+        tc, td = ctypes.c_double(), ctypes.c_double()
+        L.ref_legacy_roundtrip(m, x.ctypes.data, x.size, out.ctypes.data, 1, ctypes.byref(tc), ctypes.byref(td))
+        assert L.ref_legacy_roundtrip(m, x.ctypes.data, x.size, out.ctypes.data, reps, ctypes.byref(tc),
+                                      ctypes.byref(td)) == 0
+        per[name] = {"compress_ms": round(tc.value * 1e3, 3), "decompress_ms": round(td.value * 1e3, 3)}
+        tot += tc.value + td.value
+    value = 4.0 * x.size * len(LEGACY_NAMES) / tot / 1e9
+    return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": f"one array of {x.size} uniform[-10,10] floats per method, quantization_compress + "
+                      f"quantization_decompress of the reference's legacy library, 1 warmup + mean of {reps}",
+            "per_method": per, "nproc": nproc, "cpu_model": model, "sockets": sockets}
+
+
+def legacy_bench(args):
+    """Throughput of the legacy formats' device codecs (csrc/legacy.hip).
+
+    A step encodes and decodes the reference benches' batch (5 arrays of
+    4 194 304 uniform[-10, 10] floats, resident in HBM) with every one of the
+    13 methods through bsq_legacy_encode_device / bsq_legacy_decode_device.
+    `value` is FP32 input bytes over the timed steps' wall time.  Each
+    method's encode and decode are also bracketed by HIP events: the roofline
+    figure is algorithmic bytes (encode: 4n read + the payload written;
+    decode: the payload read + 4n written) over that time, per method and
+    over all methods."""
+    L = B.lib()
+    rng = np.random.default_rng(7)
+    xs = rng.uniform(-10.0, 10.0, LEGACY_ARRAYS * LEGACY_N).astype(np.float32)
+    dsrc = B.DeviceBuffer.from_array(xs)
+    ddst = B.DeviceBuffer(xs.nbytes)
+    sizes = {m: B.legacy_payload_bytes(m, LEGACY_N) for m in LEGACY_NAMES}
+    pitch = (max(sizes.values()) + 255) // 256 * 256
+    dimg = B.DeviceBuffer(pitch * LEGACY_ARRAYS)
+    print(f"bench: legacy formats, {LEGACY_ARRAYS} x {LEGACY_N} floats", file=sys.stderr, flush=True)
+
+    def run(m, a):
+        src = dsrc.value + 4 * a * LEGACY_N
+        img = dimg.value + pitch * a
+        B.check(L.bsq_legacy_encode_device(m, src, LEGACY_N, img, None), "legacy encode")
+        B.check(L.bsq_legacy_decode_device(m, img, LEGACY_N, ddst.value + 4 * a * LEGACY_N, None), "legacy decode")
+
+    def step():
+        for m in LEGACY_NAMES:
+            for a in range(LEGACY_ARRAYS):
+                run(m, a)
+
+    for _ in range(args.warmup):
+        step()
+    B.device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    B.device_synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt / args.steps * 1e3
+    value = 4.0 * xs.size * len(LEGACY_NAMES) * args.steps / dt / 1e9
+
+    # per-method encode / decode times with HIP events (same stream), and a
+    # spot check of the last decode against the oracle's
+    ev = [B.Event() for _ in range(3)]
+    per, tot_bytes, tot_ms = {}, 0.0, 0.0
+    reps = max(3, args.steps)
+    for m, name in LEGACY_NAMES.items():
+        enc = dec = 0.0
+        for _ in range(reps):
+            for a in range(LEGACY_ARRAYS):
+                src = dsrc.value + 4 * a * LEGACY_N
+                img = dimg.value + pitch * a
+                ev[0].record()
+                B.check(L.bsq_legacy_encode_device(m, src, LEGACY_N, img, None), "legacy encode")
+                ev[1].record()
+                B.check(L.bsq_legacy_decode_device(m, img, LEGACY_N, ddst.value + 4 * a * LEGACY_N, None), "decode")
+                ev[2].record()
+                B.check(L.bsq_stream_synchronize(None), "sync")
+                enc += ev[0].elapsed_ms(ev[1])
+                dec += ev[1].elapsed_ms(ev[2])
+        launches = reps * LEGACY_ARRAYS
+        enc, dec = enc / launches, dec / launches
+        alg = 4.0 * LEGACY_N + sizes[m]
+        per[name] = {"encode_us": round(enc * 1e3, 2), "decode_us": round(dec * 1e3, 2),
+                     "alg_bytes": int(alg), "payload_bytes": sizes[m],
+                     "encode_gbs": round(alg / (enc * 1e-3) / 1e9, 1), "decode_gbs": round(alg / (dec * 1e-3) / 1e9, 1),
+                     "encode_frac": round(alg / (enc * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "decode_frac": round(alg / (dec * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        tot_bytes += 2 * alg
+        tot_ms += enc + dec
+    achieved = tot_bytes / (tot_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "legacy.hip encode + decode launches of all 13 methods (HIP events per call)",
+                "avg_ms": round(tot_ms / (2 * len(LEGACY_NAMES)), 5), "per_method": per}
+    line = {
+        "metric": "legacy formats compress+decompress GB/s (FP32 in), 5 x 4194304 uniform[-10,10] per method",
+        "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "legacy_formats", "arrays": LEGACY_ARRAYS, "elements": LEGACY_N,
+                   "methods": list(LEGACY_NAMES.values()), "input": "device-resident"},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = legacy_cpu_baseline(xs[:LEGACY_N].copy())
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -273,12 +407,17 @@ def main():
     ap.add_argument("--workload", default="headline", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--legacy", action="store_true",
+                    help="measure the legacy formats' device codecs instead of the packed-object pipeline")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only; the multi-GPU design (row shards, one "
               "all-reduce per NF4_DQ section and per power iteration) is described in DESIGN.md",
               file=sys.stderr)
         sys.exit(2)
+    if args.legacy:
+        legacy_bench(args)
+        return
 
     wl = WORKLOADS[args.workload]
     rows, cols, ro, re, svd, nit, uv, s, direct, gen = wl

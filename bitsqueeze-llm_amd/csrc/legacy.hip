@@ -126,9 +126,24 @@ __device__ __forceinline__ long long lrint_x86(float v) {
     const float r = __builtin_rintf(v);
     return (fabsf(r) < 9.223372036854775808e18f) ? static_cast<long long>(r) : LLONG_MIN;
 }
-// (int)lrintf(v): the low 32 bits of the long.
+// (int)lrintf(v): the low 32 bits of the long (0 for NaN and |v| >= 2^63).
+// Branch-free: outside the int32 range r = m * 2^(e - 23) with e >= 31, whose
+// low 32 bits are m << (e - 23) for e < 55 and 0 from there on.
 __device__ __forceinline__ int lrint_int(float v) {
-    return static_cast<int>(static_cast<uint32_t>(static_cast<unsigned long long>(lrint_x86(v))));
+    const float r = __builtin_rintf(v);
+    const uint32_t b = __float_as_uint(r);
+    const int e = static_cast<int>((b >> 23) & 0xFFu) - 127;
+    const uint32_t m = (b & 0x7FFFFFu) | 0x800000u;
+    uint32_t lo = (e >= 31 && e < 55) ? (m << static_cast<uint32_t>(e - 23 < 0 ? 0 : e - 23)) : 0u;
+    lo = (b >> 31) ? (0u - lo) : lo;
+    return fabsf(r) < 2147483648.0f ? static_cast<int>(r) : static_cast<int>(lo);
+}
+// clamp(lrintf(v), -lim, lim) with the long result of the x86-64 build:
+// NaN and |v| >= 2^63 give LONG_MIN, which clamps to -lim.
+__device__ __forceinline__ int lrint_clamp(float v, float lim) {
+    const float r = __builtin_rintf(v);
+    if (!(fabsf(r) < 9.223372036854775808e18f)) return -static_cast<int>(lim);
+    return static_cast<int>(r < -lim ? -lim : (r > lim ? lim : r));
 }
 
 // FP32 -> FP16, IEEE round to nearest even, NaN -> sign | 0x7E00
@@ -336,11 +351,17 @@ __global__ void header_kernel(uint8_t *__restrict__ img, Header h, int words) {
 
 // Block-of-32 formats.  A quad of lanes is one block; the loop runs over
 // whole quads so that every shuffle partner is active.
+// Workgroup 0 writes the format struct (`hw` words of `h`) to `img`.
+__device__ __forceinline__ void write_header(uint8_t *img, const Header &h, int hw) {
+    if (blockIdx.x == 0 && threadIdx.x < static_cast<unsigned>(hw)) reinterpret_cast<uint32_t *>(img)[threadIdx.x] = h.w[threadIdx.x];
+}
+
 template <int M>
 __global__ __launch_bounds__(kLT) void blk32_encode_kernel(const float *__restrict__ x, uint64_t n, bool vec,
                                                            uint8_t *__restrict__ scales, uint8_t *__restrict__ codes,
-                                                           bool al4) {
+                                                           bool al4, uint8_t *__restrict__ img, Header h, int hw) {
     constexpr bool kNib = (M == Q4_0 || M == MXFP4);
+    write_header(img, h, hw);
     const uint64_t chunks = ceil_div(n, 8), nb = ceil_div(n, 32), span = (chunks + 3) & ~3ull;
     for (uint64_t c = gtid(); c < span; c += gstride()) {
         float v[8];
@@ -361,15 +382,13 @@ __global__ __launch_bounds__(kLT) void blk32_encode_kernel(const float *__restri
         if constexpr (M == Q8_0 || M == Q4_0) {
             // q8_0_impl.cpp:80-93, q4_0_impl.cpp:84-107
             constexpr float kDiv = (M == Q8_0) ? 127.0f : 7.0f;
-            constexpr long long kLim = (M == Q8_0) ? 127 : 7;
+            constexpr float kLim = (M == Q8_0) ? 127.0f : 7.0f;
             const float scale = (a > 0.0f) ? (a / kDiv) : 0.0f;
             const float inv = (scale > 0.0f) ? (1.0f / scale) : 0.0f;
             if (writer) reinterpret_cast<float *>(scales)[b] = scale;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                long long qi = lrint_x86(v[i] * inv);
-                qi = qi < -kLim ? -kLim : (qi > kLim ? kLim : qi);
-                q[i] = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(qi)));
+                q[i] = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(lrint_clamp(v[i] * inv, kLim))));
             }
         } else if constexpr (M == MXFP8) {
             // mxfp8_impl.cpp:144-157: elements divided by 2^e
@@ -419,20 +438,26 @@ __global__ __launch_bounds__(kLT) void blk32_decode_kernel(const uint8_t *__rest
 }
 
 // Largest finite |x| (fp8_impl.cpp:103-114): one atomic max per workgroup on
-// the bit pattern (non-negative floats order as their bits).
+// the bit pattern (non-negative floats order as their bits).  Launched with
+// at most one workgroup per CU (device-scope atomics on one word serialise
+// across the XCDs); each lane keeps 4 chunk loads in flight.
 __global__ __launch_bounds__(kLT) void finite_absmax_kernel(const float *__restrict__ x, uint64_t n, bool vec,
                                                             uint32_t *__restrict__ word) {
     __shared__ float red[kLT / 64];
-    const uint64_t chunks = ceil_div(n, 8);
+    constexpr int kU = 4;
+    const uint64_t chunks = ceil_div(n, 8), stride = gstride();
     float a = 0.0f;
-    for (uint64_t c = gtid(); c < chunks; c += gstride()) {
-        float v[8];
-        load8(x, c, n, vec, v);
+    for (uint64_t c0 = gtid(); c0 < chunks; c0 += kU * stride) {
+        float v[kU][8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float f = __builtin_isfinite(v[i]) ? fabsf(v[i]) : 0.0f;
-            if (f > a) a = f;
-        }
+        for (int u = 0; u < kU; ++u) load8(x, c0 + u * stride, n, vec, v[u]);
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float f = __builtin_isfinite(v[u][i]) ? fabsf(v[u][i]) : 0.0f;
+                if (f > a) a = f;
+            }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) a = max_if_greater(a, __shfl_xor(a, off));
@@ -535,14 +560,24 @@ __global__ __launch_bounds__(kLT) void nvfp4_decode_kernel(const float *__restri
     }
 }
 
+// clamp((int)lrintf(v), 0, 3).  With `small` (every |v| below 2^30, a bound
+// the caller proves for the whole block) the int32 conversion is exact and
+// NaN converts to 0 as on the host; otherwise the exact low-word rule.
+__device__ __forceinline__ int code2(float v, bool small) {
+    const int l = small ? static_cast<int>(__builtin_rintf(v)) : lrint_int(v);
+    return l < 0 ? 0 : (l > 3 ? 3 : l);
+}
+
 // Weighted least-squares block fit of Q2_K (q2_k_impl.cpp:59-140).
 __device__ __forceinline__ void q2k_fit(const float w[16], float &scale_out, float &min_out) {
     float mn = w[0], mx = w[0], sw = fabsf(w[0]), sx = sw * w[0];
+    float lo = w[0];  // the block's own minimum (mn is clipped at 0 below and later replaced)
 #pragma unroll
     for (int i = 1; i < 16; ++i) {
         const float aw = fabsf(w[i]);
         if (w[i] < mn) mn = w[i];
         if (w[i] > mx) mx = w[i];
+        if (w[i] < lo) lo = w[i];
         sw += aw;
         sx += aw * w[i];
     }
@@ -554,21 +589,26 @@ __device__ __forceinline__ void q2k_fit(const float w[16], float &scale_out, flo
     }
     float iscale = 3.0f / (mx - mn);
     float best_scale = 1.0f / iscale, best_err = 0.0f;
+    // every non-NaN w lies in [lo, mx], so |iscale (w - mn)| <= |iscale| dev
+    auto small_for = [&](float isc) {
+        const float dev = fmaxf(fabsf(mx - mn), fabsf(lo - mn));
+        return fabsf(isc) * dev < 1073741824.0f;
+    };
+    bool small = small_for(iscale);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        int l = lrint_int(iscale * (w[i] - mn));
-        l = l < 0 ? 0 : (l > 3 ? 3 : l);
+        const int l = code2(iscale * (w[i] - mn), small);
         best_err += fabsf(w[i]) * fabsf(best_scale * static_cast<float>(l) + mn - w[i]);
     }
 #pragma unroll 1
     for (int is = 0; is <= 15; ++is) {
         iscale = (-0.5f + 0.1f * static_cast<float>(is) + 3.0f) / (mx - mn);
+        small = small_for(iscale);
         float sl = 0, sl2 = 0, sxl = 0;
         uint32_t la = 0;  // 16 two-bit codes
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            int l = lrint_int(iscale * (w[i] - mn));
-            l = l < 0 ? 0 : (l > 3 ? 3 : l);
+            const int l = code2(iscale * (w[i] - mn), small);
             la |= static_cast<uint32_t>(l) << (2 * i);
             const float aw = fabsf(w[i]), fl = static_cast<float>(l);
             sl += aw * fl;
@@ -621,7 +661,9 @@ __device__ __forceinline__ void q2k_fit_fast(const float w[16], float &scale_out
 // 20 + 32 (j / 8) + 16 (j % 2) + i with shift 2 ((j % 8) / 2).
 template <bool FAST>
 __global__ __launch_bounds__(kLT) void q2k_encode_kernel(const float *__restrict__ x, uint64_t n, bool vec,
-                                                         uint8_t *__restrict__ rec) {
+                                                         uint8_t *__restrict__ rec, uint8_t *__restrict__ img,
+                                                         Header h, int hw) {
+    write_header(img, h, hw);
     const uint64_t nsb = ceil_div(n, 256);
     const int j = static_cast<int>(threadIdx.x & 15);
     for (uint64_t t = gtid(); t < nsb * 16; t += gstride()) {
@@ -667,11 +709,18 @@ __global__ __launch_bounds__(kLT) void q2k_encode_kernel(const float *__restrict
         const float tmn = fp16_to_f32(sm) * static_cast<float>(mq);
         const uint32_t shift = 2u * static_cast<uint32_t>((j & 7) >> 1);
         uint32_t cw[4] = {0u, 0u, 0u, 0u};
+        // |(w - tmn) / tsc| <= dev / tsc for every non-NaN w of the block
+        float blo = w[0], bhi = w[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+            blo = w[i] < blo ? w[i] : blo;
+            bhi = w[i] > bhi ? w[i] : bhi;
+        }
+        const bool small = !(tsc > 0.0f) || fmaxf(fabsf(bhi - tmn), fabsf(blo - tmn)) < 1073741824.0f * tsc;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const float v = (tsc > 0.0f) ? (w[i] - tmn) / tsc : 0.0f;
-            int l = lrint_int(v);
-            l = l < 0 ? 0 : (l > 3 ? 3 : l);
+            const int l = code2(v, small);
             cw[i >> 2] |= (static_cast<uint32_t>(l) << shift) << (8 * (i & 3));
         }
         // OR the four contributions (lanes j, j ^ 2, j ^ 4, j ^ 6 share bytes)
@@ -725,7 +774,9 @@ __global__ __launch_bounds__(kLT) void q2k_decode_kernel(const uint8_t *__restri
 
 template <bool FP16>
 __global__ __launch_bounds__(kLT) void half_encode_kernel(const float *__restrict__ x, uint64_t n, bool vec,
-                                                          uint16_t *__restrict__ q) {
+                                                          uint16_t *__restrict__ q, uint8_t *__restrict__ img,
+                                                          Header h, int hw) {
+    write_header(img, h, hw);
     const uint64_t chunks = ceil_div(n, 8);
     for (uint64_t c = gtid(); c < chunks; c += gstride()) {
         float v[8];
@@ -785,8 +836,8 @@ __global__ __launch_bounds__(kLT) void legacy_sweep_kernel(int kind, uint64_t lo
     if ((threadIdx.x & 63) == 0) atomicAdd(out, acc);
 }
 
-unsigned grid_for_items(uint64_t items) {
-    const uint64_t want = ceil_div(items, kLT), cap = static_cast<uint64_t>(cu_count()) * 16;
+unsigned grid_for_items(uint64_t items, uint64_t per_cu = 16) {
+    const uint64_t want = ceil_div(items, kLT), cap = static_cast<uint64_t>(cu_count()) * per_cu;
     return static_cast<unsigned>(want < 1 ? 1 : (want < cap ? want : cap));
 }
 
@@ -811,18 +862,25 @@ void launch_legacy_encode(int method, const float *x, uint64_t n, uint8_t *img, 
     uint8_t *a = img + L.a_off, *b = img + L.b_off;
     const bool al4 = al(method == Q2_K || method == Q2_K_FAST || method == BF16 || method == FP16 ||
                                 method == FP8 || method == FP4 ? a : b, 4);
-    header_kernel<<<1, 64, 0, st>>>(img, header_of(method, n, L), static_cast<int>(L.header / 4));
-    BSQ_HIP(hipGetLastError());
-    const unsigned g8 = grid_for_items(ceil_div(n, 8) + 3);
+    const Header h = header_of(method, n, L);
+    const int hw = static_cast<int>(L.header / 4);
+    // formats with a reduction pass (or the packed object's codec) write the
+    // struct first: it also zeroes the scratch word
+    const bool separate_header = method == FP8 || method == FP4 || method == NVFP4 || method == NF4 || method == NF4_DQ;
+    if (separate_header) {
+        header_kernel<<<1, 64, 0, st>>>(img, h, hw);
+        BSQ_HIP(hipGetLastError());
+    }
+    const unsigned g8 = grid_for_items(ceil_div(n, 8) + 3), g1 = grid_for_items(ceil_div(n, 8), 1);
     uint32_t *word = L.scratch_off >= 0 ? reinterpret_cast<uint32_t *>(img + L.scratch_off) : nullptr;
     switch (method) {
-        case Q8_0: blk32_encode_kernel<Q8_0><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4); break;
-        case Q4_0: blk32_encode_kernel<Q4_0><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4); break;
-        case MXFP8: blk32_encode_kernel<MXFP8><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4); break;
-        case MXFP4: blk32_encode_kernel<MXFP4><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4); break;
+        case Q8_0: blk32_encode_kernel<Q8_0><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4, img, h, hw); break;
+        case Q4_0: blk32_encode_kernel<Q4_0><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4, img, h, hw); break;
+        case MXFP8: blk32_encode_kernel<MXFP8><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4, img, h, hw); break;
+        case MXFP4: blk32_encode_kernel<MXFP4><<<g8, kLT, 0, st>>>(x, n, vec, a, b, al4, img, h, hw); break;
         case FP8:
         case FP4:
-            finite_absmax_kernel<<<g8, kLT, 0, st>>>(x, n, vec, word);
+            finite_absmax_kernel<<<g1, kLT, 0, st>>>(x, n, vec, word);
             BSQ_HIP(hipGetLastError());
             if (method == FP8)
                 gscale_encode_kernel<false><<<g8, kLT, 0, st>>>(x, n, vec, word,
@@ -832,7 +890,7 @@ void launch_legacy_encode(int method, const float *x, uint64_t n, uint8_t *img, 
                                                                reinterpret_cast<float *>(img + L.scale_off), a, al4);
             break;
         case NVFP4:
-            finite_absmax_kernel<<<g8, kLT, 0, st>>>(x, n, vec, word);
+            finite_absmax_kernel<<<g1, kLT, 0, st>>>(x, n, vec, word);
             BSQ_HIP(hipGetLastError());
             nvfp4_encode_kernel<<<g8, kLT, 0, st>>>(x, n, vec, word, reinterpret_cast<float *>(img + L.scale_off), a, b,
                                                     al(b, 4));
@@ -840,12 +898,16 @@ void launch_legacy_encode(int method, const float *x, uint64_t n, uint8_t *img, 
         case Q2_K:
         case Q2_K_FAST: {
             const unsigned g = grid_for_items(ceil_div(n, 256) * 16);
-            if (method == Q2_K) q2k_encode_kernel<false><<<g, kLT, 0, st>>>(x, n, vec, a);
-            else q2k_encode_kernel<true><<<g, kLT, 0, st>>>(x, n, vec, a);
+            if (method == Q2_K) q2k_encode_kernel<false><<<g, kLT, 0, st>>>(x, n, vec, a, img, h, hw);
+            else q2k_encode_kernel<true><<<g, kLT, 0, st>>>(x, n, vec, a, img, h, hw);
             break;
         }
-        case BF16: half_encode_kernel<false><<<g8, kLT, 0, st>>>(x, n, vec, reinterpret_cast<uint16_t *>(a)); break;
-        case FP16: half_encode_kernel<true><<<g8, kLT, 0, st>>>(x, n, vec, reinterpret_cast<uint16_t *>(a)); break;
+        case BF16:
+            half_encode_kernel<false><<<g8, kLT, 0, st>>>(x, n, vec, reinterpret_cast<uint16_t *>(a), img, h, hw);
+            break;
+        case FP16:
+            half_encode_kernel<true><<<g8, kLT, 0, st>>>(x, n, vec, reinterpret_cast<uint16_t *>(a), img, h, hw);
+            break;
         case NF4:
             launch_quant_encode(x, n, kMethodNF4, reinterpret_cast<float *>(a), nullptr, nullptr, b, nullptr, st);
             break;

@@ -385,7 +385,9 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
     } else if (method == kMethodNF4DQ) {
         BSQ_REQUIRE(scales_u8 && codes && dq_out && gmax_scratch, "quant encode: null NF4_DQ output");
         BSQ_HIP(hipMemsetAsync(gmax_scratch, 0, sizeof(uint32_t), stream));
-        dq_gmax_kernel<<<grid, kThreads, 0, stream>>>(x, n, vec_ok, gmax_scratch);
+        // one workgroup per CU: every workgroup ends in one device-scope
+        // atomic on the same word, and those serialise across the XCDs
+        dq_gmax_kernel<<<grid_for(ceil_div(n, 8), 1), kThreads, 0, stream>>>(x, n, vec_ok, gmax_scratch);
         quant_encode_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8, gmax_scratch,
                                                                  dq_out, codes);
     } else {
