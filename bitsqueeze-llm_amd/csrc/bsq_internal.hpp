@@ -84,6 +84,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f32,
                          uint8_t *scales_u8, float *dq_out, uint8_t *codes,
                          uint32_t *gmax_scratch, hipStream_t stream);
+// NF4_DQ encode whose global max of the block absmax is already known per row
+// (row_gmax[0 .. rows), from the outlier separation): one small reduce, then
+// the encode pass; the same bytes as launch_quant_encode.
+void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gmax, uint32_t rows,
+                                 uint8_t *scales_u8, float *dq_out, uint8_t *codes, uint32_t *gmax_scratch,
+                                 hipStream_t stream);
 void launch_quant_decode(uint64_t n, int method, const float *scales_f32,
                          const uint8_t *scales_u8, const float *dq, const uint8_t *codes,
                          float *out, hipStream_t stream);
@@ -114,9 +120,16 @@ struct TopkArgs {
     float *values = nullptr;          // rows x k
     float *residual = nullptr;        // optional: a with the selected entries zeroed
     uint32_t *flags = nullptr;        // optional: OR kFlagError if any |v| > FLT_EPSILON
+    // optional, with `residual`: row_gmax[r] = max over the residual's
+    // 64-element blocks of row r of the block's largest sanitised |value|
+    // (1 for an all-zero block), the per-row part of NF4_DQ's global scale
+    float *row_gmax = nullptr;
     TopkSource source = TopkSource::Dense;
 };
-void launch_topk_select(const TopkArgs &args, hipStream_t stream);
+// Returns true when row_gmax was requested and written (the register-resident
+// kernel on a Dense source with cols % 64 == 0); otherwise row_gmax is left
+// alone and the caller computes the global scale itself.
+bool launch_topk_select(const TopkArgs &args, hipStream_t stream);
 // Largest k the single-workgroup LDS sort handles; larger k (up to the row
 // length) is sorted in bands of this many ranks.
 constexpr uint32_t kTopkMaxK = 8192;

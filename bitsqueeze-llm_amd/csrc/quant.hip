@@ -396,6 +396,33 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
     BSQ_HIP(hipGetLastError());
 }
 
+namespace {
+// *gmax = bits of max_r row_gmax[r] (one workgroup; max is order-free).
+__global__ __launch_bounds__(kThreads) void rows_gmax_kernel(const float *__restrict__ row_gmax, uint32_t rows,
+                                                             uint32_t *__restrict__ gmax) {
+    __shared__ float red[kThreads / 64];
+    float m = 0.0f;
+    for (uint32_t i = threadIdx.x; i < rows; i += kThreads) m = fmaxf(m, row_gmax[i]);
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) *gmax = __float_as_uint(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+}  // namespace
+
+void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gmax, uint32_t rows,
+                                 uint8_t *scales_u8, float *dq_out, uint8_t *codes, uint32_t *gmax_scratch,
+                                 hipStream_t stream) {
+    BSQ_REQUIRE(n > 0 && rows > 0 && row_gmax && scales_u8 && codes && dq_out && gmax_scratch,
+                "quant encode: bad NF4_DQ arguments");
+    const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
+    rows_gmax_kernel<<<1, kThreads, 0, stream>>>(row_gmax, rows, gmax_scratch);
+    BSQ_HIP(hipGetLastError());
+    quant_encode_kernel<true><<<grid_for(ceil_div(n, 8)), kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8,
+                                                                                 gmax_scratch, dq_out, codes);
+    BSQ_HIP(hipGetLastError());
+}
+
 void launch_quant_decode(uint64_t n, int method, const float *scales_f32, const uint8_t *scales_u8,
                          const float *dq, const uint8_t *codes, float *out, hipStream_t stream) {
     BSQ_REQUIRE(n > 0, "quant decode: empty output");

@@ -142,6 +142,7 @@ struct Runtime {
     float *d_stage = nullptr;     // HOST-input staging
     float *d_residual = nullptr;  // input with outliers zeroed
     float *d_err = nullptr;       // residual - U S V^T (SVD path with error top-k)
+    float *d_row_gmax = nullptr;  // per-row NF4_DQ block maxima from the outlier separation
     Section sec[4];
     TopkBuf topk[2];
     Meta *meta = nullptr;
@@ -168,6 +169,7 @@ struct Runtime {
         dev_free(d_stage);
         dev_free(d_residual);
         dev_free(d_err);
+        dev_free(d_row_gmax);
         dev_free(meta);
         dev_free(q_scales_f32);
         dev_free(q_scales_u8);
@@ -360,6 +362,7 @@ void compress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int s
         sc.method = direct;
         sc.count = N;
         if (sc.method != kMethodNone) sc.alloc_quant();
+        if (direct == kMethodNF4DQ && rt.topk[TK_OUTLIER].capacity > 0) rt.d_row_gmax = dev_alloc<float>(rows);
     }
     alloc_host_stage(rt);
     BSQ_HIP(hipStreamSynchronize(rt.stream));
@@ -434,6 +437,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
 
     // outlier separation (topk_separation, src/bitsqz_llm.cu:1045-1056)
     const float *residual = d_in;
+    bool have_row_gmax = false;
     TopkBuf &to = rt.topk[TK_OUTLIER];
     if (to.capacity > 0) {
         TopkArgs a;
@@ -444,7 +448,10 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
         a.indices = to.idx;
         a.values = to.val;
         a.residual = rt.d_residual;
-        launch_topk_select(a, st);
+        // the direct NF4_DQ section's global scale needs the largest block
+        // absmax of the residual: the separation kernel reports it per row
+        a.row_gmax = rt.d_row_gmax;
+        have_row_gmax = launch_topk_select(a, st);
         residual = rt.d_residual;
         flags |= kFlagOutlier;
     }
@@ -498,8 +505,12 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
         BSQ_HIP(hipEventRecord(rt.ev[2], st));
         if (D.method != kMethodNone) {
             D.dense = nullptr;
-            launch_quant_encode(residual, N, D.method, D.scales_f32, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
-                                D.codes, &rt.meta->gmax, st);
+            if (have_row_gmax && D.method == kMethodNF4DQ)
+                launch_quant_encode_dq_rows(residual, N, rt.d_row_gmax, rows, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
+                                            D.codes, &rt.meta->gmax, st);
+            else
+                launch_quant_encode(residual, N, D.method, D.scales_f32, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
+                                    D.codes, &rt.meta->gmax, st);
             BSQ_HIP(hipEventRecord(rt.ev[3], st));
             BSQ_HIP(hipEventRecord(rt.ev[4], st));
             BSQ_HIP(hipEventRecord(rt.ev[5], st));

@@ -15,6 +15,7 @@
 // HBM once; `v` can be computed on the fly as a - b or as a - dequant(NF4)
 // so that the error-correction pass never materialises the error matrix.
 #include "bsq_internal.hpp"
+#include "wave_ops.hpp"
 
 #include <algorithm>
 #include <cfloat>
@@ -114,6 +115,7 @@ struct Shared {
     uint32_t ncand;
     unsigned long long kt, kth;  // filter threshold, k-th largest composite key (fast path)
     float L[16];
+    float wmax[kThreads / 64];  // per-wave maxima of the row's NF4_DQ block maxima
 };
 
 // Fast path (row cached, k <= 256): at most this many candidates are ranked
@@ -705,36 +707,42 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         const unsigned long long kth = sh.kth;
         float4 *res4 = reinterpret_cast<float4 *>(a.residual + row0);
         lt = lane_id();
-        if ((kth >> 16) != 0) {  // uniform: the k-th largest is a number
-            const MagThreshold mk(kth);
+        const bool kth_number = (kth >> 16) != 0;  // uniform: the k-th largest is a number
+        const MagThreshold mk(kth_number ? kth : (1ull << 16));
+        // with row_gmax (cols % 64 == 0): a 64-element block is the quads of
+        // 16 consecutive lanes (one DPP row) at one m, its absmax a 4-step
+        // DPP max
+        float gm = 0.0f;
 #pragma unroll
-            for (int m = 0; m < NV4; ++m) {
-                const uint32_t c4 = lt + kThreads * m;
-                if (c4 < q4) {
-                    const uint32_t c = 4 * c4;
-                    float4 o;
-                    o.x = mk.reaches(v[m][0], c + 0) ? 0.0f : v[m][0];
-                    o.y = mk.reaches(v[m][1], c + 1) ? 0.0f : v[m][1];
-                    o.z = mk.reaches(v[m][2], c + 2) ? 0.0f : v[m][2];
-                    o.w = mk.reaches(v[m][3], c + 3) ? 0.0f : v[m][3];
-                    res4[c4] = o;
-                }
-                __builtin_amdgcn_sched_barrier(0);
+        for (int m = 0; m < NV4; ++m) {
+            const uint32_t c4 = lt + kThreads * m;
+            float4 o;
+            if (kth_number) {
+                const uint32_t c = 4 * c4;
+                o.x = mk.reaches(v[m][0], c + 0) ? 0.0f : v[m][0];
+                o.y = mk.reaches(v[m][1], c + 1) ? 0.0f : v[m][1];
+                o.z = mk.reaches(v[m][2], c + 2) ? 0.0f : v[m][2];
+                o.w = mk.reaches(v[m][3], c + 3) ? 0.0f : v[m][3];
+            } else {
+                o.x = (key_of(lt, m, 0) >= kth) ? 0.0f : v[m][0];
+                o.y = (key_of(lt, m, 1) >= kth) ? 0.0f : v[m][1];
+                o.z = (key_of(lt, m, 2) >= kth) ? 0.0f : v[m][2];
+                o.w = (key_of(lt, m, 3) >= kth) ? 0.0f : v[m][3];
             }
-        } else {
-#pragma unroll
-            for (int m = 0; m < NV4; ++m) {
-                const uint32_t c4 = lt + kThreads * m;
-                if (c4 < q4) {
-                    float4 o;
-                    o.x = (key_of(lt, m, 0) >= kth) ? 0.0f : v[m][0];
-                    o.y = (key_of(lt, m, 1) >= kth) ? 0.0f : v[m][1];
-                    o.z = (key_of(lt, m, 2) >= kth) ? 0.0f : v[m][2];
-                    o.w = (key_of(lt, m, 3) >= kth) ? 0.0f : v[m][3];
-                    res4[c4] = o;
-                }
-                __builtin_amdgcn_sched_barrier(0);
+            if (c4 < q4) res4[c4] = o;
+            if (a.row_gmax) {  // uniform
+                auto san = [](float x) { return __builtin_isfinite(x) ? fabsf(x) : 0.0f; };
+                const float bm = row16_max(fmaxf(fmaxf(san(o.x), san(o.y)), fmaxf(san(o.z), san(o.w))));
+                if (c4 < q4) gm = fmaxf(gm, bm > 0.0f ? bm : 1.0f);
             }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (a.row_gmax) {
+            for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+            __syncthreads();
+            if ((tid & 63) == 0) sh.wmax[tid >> 6] = gm;
+            __syncthreads();
+            if (tid == 0) a.row_gmax[r] = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
         }
     }
 }
@@ -886,15 +894,21 @@ void launch_reg(const TopkArgs &a, hipStream_t stream) {
     topk_reg_kernel<SRC, NV4><<<a.rows, kThreads, 0, stream>>>(a);
 }
 
+// Whether the register-resident kernel serves this shape: rows up to 11264
+// columns (44 values per lane, about 120 VGPRs: four rows per CU, one more
+// than the LDS-cached kernel fits); longer rows would pass 128 VGPRs and
+// halve the resident rows.
+bool reg_eligible(const TopkArgs &a) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a.a) | reinterpret_cast<uintptr_t>(a.residual) |
+                         (a.source == TopkSource::DenseMinusDense ? reinterpret_cast<uintptr_t>(a.b) : 0);
+    if (a.k > kTopkMaxK || (a.cols & 3u) != 0 || (al & 15u) != 0 || a.k > kThreads || a.k > a.cols / 4) return false;
+    return ceil_div(a.cols / 4, kThreads) <= 11;
+}
+
 // True (and launched) when the register-resident kernel serves this shape.
 template <TopkSource SRC>
 bool try_launch_reg(const TopkArgs &a, hipStream_t stream) {
-    const uintptr_t al = reinterpret_cast<uintptr_t>(a.a) | reinterpret_cast<uintptr_t>(a.residual) |
-                         (SRC == TopkSource::DenseMinusDense ? reinterpret_cast<uintptr_t>(a.b) : 0);
-    if ((a.cols & 3u) != 0 || (al & 15u) != 0 || a.k > kThreads || a.k > a.cols / 4) return false;
-    // rows up to 11264 columns (44 values per lane, about 120 VGPRs: four
-    // rows per CU, one more than the LDS-cached kernel fits); longer rows
-    // would pass 128 VGPRs and halve the resident rows
+    if (!reg_eligible(a)) return false;
     const uint32_t nv4 = static_cast<uint32_t>(ceil_div(a.cols / 4, kThreads));
     if (nv4 <= 2) launch_reg<SRC, 2>(a, stream);
     else if (nv4 <= 4) launch_reg<SRC, 4>(a, stream);
@@ -984,7 +998,11 @@ void launch_src(const TopkArgs &a, hipStream_t stream) {
 
 }  // namespace
 
-void launch_topk_select(const TopkArgs &a, hipStream_t stream) {
+bool launch_topk_select(const TopkArgs &args, hipStream_t stream) {
+    TopkArgs a = args;
+    const bool gmax = a.row_gmax && a.residual && a.source == TopkSource::Dense && a.cols % 64 == 0 &&
+                      reg_eligible(a);
+    if (!gmax) a.row_gmax = nullptr;
     BSQ_REQUIRE(a.rows > 0 && a.cols > 0 && a.cols <= 65535 && a.rows <= 65535, "top-k: bad shape");
     BSQ_REQUIRE(a.k >= 1 && a.k <= a.cols, "top-k: k must be in [1, cols]");
     BSQ_REQUIRE(a.a && a.indices && a.values, "top-k: null pointer");
@@ -1004,6 +1022,7 @@ void launch_topk_select(const TopkArgs &a, hipStream_t stream) {
             break;
     }
     BSQ_HIP(hipGetLastError());
+    return gmax;
 }
 
 void launch_topk_scatter(const uint16_t *idx0, const float *val0, uint32_t k0, const uint16_t *idx1,

@@ -38,4 +38,20 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
     return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 
+// float v of the lane selected by the DPP control CTRL (all rows, all banks).
+template <int CTRL>
+__device__ __forceinline__ float dpp_read_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// fmaxf over each aligned group of 16 lanes (one DPP row), in every lane of
+// the group; all 16 lanes must be active.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_read_f32<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_read_f32<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_read_f32<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_read_f32<0x140>(v));  // row_mirror
+    return v;
+}
+
 }  // namespace bsq

@@ -91,6 +91,30 @@ def test_config2_4096x4096_nf4dq_outliers():
     assert out.tobytes() == exp_out.tobytes()
 
 
+@pytest.mark.parametrize("rows,cols", [(48, 4096), (40, 1000), (16, 11008)])
+def test_nf4dq_global_scale_from_the_outlier_separation(rows, cols):
+    """The direct NF4_DQ section's global scale comes from the outlier
+    separation kernel's per-row block maxima when cols % 64 == 0 (and from the
+    separate reduction otherwise): bytes and decode equal the oracle's with
+    all-zero blocks (which count as 1), NaN and infinity left in the residual
+    (sanitised to 0), and the largest block absmax in different rows."""
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows, cols)) * 0.01).astype(np.float32)
+    x[0, :192] = 0.0                        # all-zero blocks in row 0
+    x[rows // 2] *= 500.0                    # the largest residual block sits in one row
+    x[1, 5], x[2, 70] = np.nan, np.inf       # NaN is never an outlier; +inf is
+    x[3, 9] = -np.inf
+    data, out, _ = run_direct(x, 0.01, 0.02, B.NF4_DQ)
+    exp_bytes, exp_out = oracle_direct(x, 0.01, 0.02, B.NF4_DQ)
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+    # no outlier selection: the separate reduction
+    data, out, _ = run_direct(x, 0.0, 0.02, B.NF4_DQ)
+    exp_bytes, exp_out = oracle_direct(x, 0.0, 0.02, B.NF4_DQ)
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+
+
 def test_error_section_absent_when_exact():
     """A matrix the NF4 codec reproduces exactly has no error section even with
     error top-k enabled (has_nonzero gate, src/bitsqz_llm.cu:1210-1225)."""
