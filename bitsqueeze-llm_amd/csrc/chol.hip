@@ -156,8 +156,7 @@ __device__ __forceinline__ bool gj_factor16(const double (*S)[PITCH], double (*L
 }
 
 // Factors the 32 x 32 diagonal block in Dg (lower triangle used) on one wave
-// and writes its inverse to LI (zeros above the diagonal) and to LIblk (and
-// in FP32 to LIblk32 when given), by
+// and writes its inverse to LI (zeros above the diagonal) and to LIblk, by
 // 2 x 2 blocks of 16:
 //   L11, L11^{-1} = gj_factor16(A11);   L21 = A21 L11^{-T};
 //   L22, L22^{-1} = gj_factor16(A22 - L21 L21^T);
@@ -170,8 +169,7 @@ __device__ __forceinline__ bool gj_factor16(const double (*S)[PITCH], double (*L
 // Returns true when a pivot is <= tiny (or NaN).
 template <int PITCH>
 __device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*LI)[PITCH],
-                                                  double *__restrict__ LIblk, float *__restrict__ LIblk32,
-                                                  double tiny, int lane) {
+                                                  double *__restrict__ LIblk, double tiny, int lane) {
     const int kq = lane >> 4, cc = lane & 15;
     bool bad = gj_factor16<PITCH>(Dg, LI, tiny, lane);
 #pragma unroll
@@ -218,16 +216,13 @@ __device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*
     for (int u = 0; u < 16; ++u) {
         const int e = 64 * u + lane, r = e >> 5, c = e & 31;
         LIblk[e] = LI[r][c];
-        if (LIblk32) LIblk32[e] = static_cast<float>(LI[r][c]);
     }
     return bad;
 }
 
 // Lout: KP x KP row-major, the blocks below the diagonal blocks written (the
 // triangular inverse reads nothing else).  LIout: NB blocks of 32 x 32, the
-// inverses of the diagonal blocks of L (zeros above the diagonal).  L32 and
-// LI32, when given, receive the same values rounded to FP32 (the operands of
-// the blocked forward substitution).
+// inverses of the diagonal blocks of L (zeros above the diagonal).
 // status[0]: number of shifted restarts (7 = gave up, L = I).
 //
 // Right-looking by 32-column panels with look-ahead.  Wave 0 only factors the
@@ -250,8 +245,6 @@ template <int NB>
 __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double *__restrict__ G, int k,
                                                                      double *__restrict__ Lout,
                                                                      double *__restrict__ LIout,
-                                                                     float *__restrict__ L32,
-                                                                     float *__restrict__ LI32,
                                                                      int *__restrict__ status,
                                                                      const int *__restrict__ run) {
     if (run && run[0] == 0) return;  // uniform: the refinement step replaced this pass
@@ -287,9 +280,7 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
 #pragma unroll 1
             for (int jb = 0; jb < NB; ++jb) {
                 const int lane = opaque(static_cast<int>(threadIdx.x)) & 63;
-                const bool bad = factor_diag_block<PITCH>(Dg, LI, LIout + static_cast<uint64_t>(jb) * 1024,
-                                                          LI32 ? LI32 + static_cast<uint64_t>(jb) * 1024 : nullptr,
-                                                          tiny, lane);
+                const bool bad = factor_diag_block<PITCH>(Dg, LI, LIout + static_cast<uint64_t>(jb) * 1024, tiny, lane);
                 if (bad && lane == 0) broke = 1;
                 __syncthreads();  // B1
                 if (broke) {
@@ -376,9 +367,7 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
 #pragma unroll
                             for (int u = 0; u < 4; ++u) {
                                 Y[pr + 4 * u + kq][lc16 + cc] = t[u];
-                                const uint64_t o = static_cast<uint64_t>(16 * I + 4 * u + kq) * KP + 16 * J + cc;
-                                Lout[o] = t[u];
-                                if (L32) L32[o] = static_cast<float>(t[u]);
+                                Lout[static_cast<uint64_t>(16 * I + 4 * u + kq) * KP + 16 * J + cc] = t[u];
                             }
                         }
                     }
@@ -437,12 +426,10 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
         for (int t = tid; t < KP * KP; t += kCholThreads) {
             const int i = t / KP, c = t % KP;
             if (c <= i) Lout[t] = (i == c) ? 1.0 : 0.0;
-            if (L32 && c <= i) L32[t] = (i == c) ? 1.0f : 0.0f;
         }
         for (int t = tid; t < NB * 1024; t += kCholThreads) {
             const int i = (t & 1023) >> 5, c = t & 31;
             LIout[t] = (i == c) ? 1.0 : 0.0;
-            if (LI32) LI32[t] = (i == c) ? 1.0f : 0.0f;
         }
     }
     if (tid == 0 && status) status[0] = attempt;
@@ -577,8 +564,9 @@ __global__ __launch_bounds__(kTrinvThreads) void trinv_kernel(const double *__re
 
 // Q = X L^{-T} by blocked forward substitution (Q L^T = X), for the
 // orthonormalisation step of CholeskyQR: with L's blocks below the diagonal
-// (L32) and the inverses of its 32 x 32 diagonal blocks (LI32), both in FP32
-// from the factorisation, block column J of Q is
+// (Lin) and the inverses of its 32 x 32 diagonal blocks (LIin), both FP64 from
+// the factorisation and rounded to FP32 as they are staged, block column J of
+// Q is
 //     Q_J = (X_J - sum_{I < J} Q_I L_JI^T) LI_J^T.
 // One workgroup per 32 rows of X (76 KB of LDS: two workgroups per CU).  Wave
 // w works on row group g = w / 2 (16 rows) and column half h = w % 2 of each
@@ -599,29 +587,37 @@ __global__ __launch_bounds__(kTrinvThreads) void trinv_kernel(const double *__re
 // operand), and even and odd steps accumulate in two chains.  Replaces the
 // triangular inverse and the X * L^{-T} product (two launches, one of them
 // latency-bound on k / 16 CUs).
-// pv[i] = src[8 i] for i < J (J <= 7): constant slot indices on every path,
+// pv[i] = src[8 i] for i < 2 J (J <= 7): constant slot indices on every path,
 // so that the slots stay in registers.
 template <int PV>
-__device__ __forceinline__ void fetch_panel(float4 (&pv)[PV], const float4 *__restrict__ src, int J) {
+__device__ __forceinline__ void fetch_panel(double2 (&pv)[PV], const double2 *__restrict__ src, int J) {
+#define BSQ_PANEL_PAIR(j)                                   \
+    case j:                                                 \
+        if constexpr (PV >= 2 * (j)) {                      \
+            pv[2 * (j) - 1] = src[8 * (2 * (j) - 1)];       \
+            pv[2 * (j) - 2] = src[8 * (2 * (j) - 2)];       \
+        }                                                   \
+        [[fallthrough]];
     switch (J) {
-        case 7: if constexpr (PV >= 7) pv[6] = src[48]; [[fallthrough]];
-        case 6: if constexpr (PV >= 6) pv[5] = src[40]; [[fallthrough]];
-        case 5: if constexpr (PV >= 5) pv[4] = src[32]; [[fallthrough]];
-        case 4: if constexpr (PV >= 4) pv[3] = src[24]; [[fallthrough]];
-        case 3: if constexpr (PV >= 3) pv[2] = src[16]; [[fallthrough]];
-        case 2: if constexpr (PV >= 2) pv[1] = src[8]; [[fallthrough]];
-        case 1: pv[0] = src[0]; [[fallthrough]];
+        BSQ_PANEL_PAIR(7)
+        BSQ_PANEL_PAIR(6)
+        BSQ_PANEL_PAIR(5)
+        BSQ_PANEL_PAIR(4)
+        BSQ_PANEL_PAIR(3)
+        BSQ_PANEL_PAIR(2)
+        BSQ_PANEL_PAIR(1)
         default: break;
     }
+#undef BSQ_PANEL_PAIR
 }
 constexpr int kSolveRows = 32;
 template <int NB>
 __global__ __launch_bounds__(256, 2) void chol_solve_kernel(const float *__restrict__ X, int M, int k,
-                                                            const float *__restrict__ L32,
-                                                            const float *__restrict__ LI32, float *__restrict__ Q) {
+                                                            const double *__restrict__ Lin,
+                                                            const double *__restrict__ LIin, float *__restrict__ Q) {
     typedef float f32x4v __attribute__((ext_vector_type(4)));
     constexpr int KP = NB * 32, QP = KP + 4, LP = (NB > 1 ? (NB - 1) * 32 : 32) + 4, TP = 36;
-    constexpr int PV = NB > 1 ? NB - 1 : 1;  // 16-byte panel loads per thread, widest panel
+    constexpr int PV = NB > 1 ? 2 * (NB - 1) : 1;  // 16-byte panel loads per thread, widest panel
     __shared__ __align__(16) float Qs[2][16][QP];   // -Q of this workgroup's rows, per row group
     __shared__ __align__(16) float Ls[32][LP];      // L_J,0..J-1
     __shared__ __align__(16) float LIs[2][32][TP];  // LI_J (buffer J % 2)
@@ -630,31 +626,38 @@ __global__ __launch_bounds__(256, 2) void chol_solve_kernel(const float *__restr
     const int kk = lane >> 4, cc = lane & 15, g = wave >> 1, h = wave & 1;
     const int r0 = blockIdx.x * kSolveRows + 16 * g;  // this wave's first row
     const int pr = tid >> 3, pc = tid & 7;             // panel row, 16-byte column phase
-    const float4 *Lv = reinterpret_cast<const float4 *>(L32);
-    const float4 *LIv = reinterpret_cast<const float4 *>(LI32);
-    float4 pv[PV], lv;
+    const double2 *Lv = reinterpret_cast<const double2 *>(Lin);
+    const double2 *LIv = reinterpret_cast<const double2 *>(LIin);
+    double2 pv[PV], lv[2];
     float xv[4];
     // loads of block column J (panel rows: PV slots, the first J used)
 #define BSQ_SOLVE_FETCH(J)                                                                          \
     do {                                                                                            \
-        const float4 *src = Lv + (static_cast<uint64_t>(32 * (J) + pr) * KP) / 4 + pc;             \
+        const double2 *src = Lv + (static_cast<uint64_t>(32 * (J) + pr) * KP) / 2 + pc;            \
         fetch_panel<PV>(pv, src, (J));                                                              \
-        lv = LIv[static_cast<uint64_t>(J) * 256 + tid];                                             \
+        lv[0] = LIv[static_cast<uint64_t>(J) * 512 + tid];                                          \
+        lv[1] = LIv[static_cast<uint64_t>(J) * 512 + 256 + tid];                                    \
         _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                             \
             const int row = r0 + 4 * kk + u, col = 32 * (J) + 16 * h + cc;                          \
             xv[u] = (row < M && col < k) ? X[static_cast<uint64_t>(row) * k + col] : 0.0f;          \
         }                                                                                           \
     } while (0)
-    for (int i = 0; i < PV; ++i) pv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < PV; ++i) pv[i] = make_double2(0.0, 0.0);
     BSQ_SOLVE_FETCH(0);
     // unrolled: every trip count and LDS offset below is a constant
 #pragma unroll
     for (int J = 0; J < NB; ++J) {
         const int b = J & 1;
 #pragma unroll
-        for (int i = 0; i < PV; ++i)  // slots >= J land in columns the update does not use
-            *reinterpret_cast<float4 *>(&Ls[pr][4 * (pc + 8 * i)]) = pv[i];
-        *reinterpret_cast<float4 *>(&LIs[b][tid >> 3][4 * (tid & 7)]) = lv;
+        for (int i = 0; i < PV; ++i)  // slots >= 2 J land in columns the update does not use
+            *reinterpret_cast<float2 *>(&Ls[pr][2 * (pc + 8 * i)]) =
+                make_float2(static_cast<float>(pv[i].x), static_cast<float>(pv[i].y));
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int t = 2 * tid + 512 * e;
+            *reinterpret_cast<float2 *>(&LIs[b][t >> 5][t & 31]) =
+                make_float2(static_cast<float>(lv[e].x), static_cast<float>(lv[e].y));
+        }
         f32x4v acc = {xv[0], xv[1], xv[2], xv[3]}, acc1 = {0.f, 0.f, 0.f, 0.f};
         __syncthreads();  // A
         if (J + 1 < NB) BSQ_SOLVE_FETCH(J + 1);
@@ -709,17 +712,16 @@ void chol_solve(const double *G, int k, double *Lbuf, const float *X, int M, flo
                 hipStream_t stream) {
     constexpr uint64_t KP = NB * 32;
     double *L = Lbuf, *LI = Lbuf + KP * KP;
-    float *L32 = reinterpret_cast<float *>(LI + NB * 1024), *LI32 = L32 + KP * KP;
-    chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, L32, LI32, status, nullptr);
+    chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, status, nullptr);
     BSQ_HIP(hipGetLastError());
-    chol_solve_kernel<NB><<<static_cast<unsigned>(ceil_div(M, kSolveRows)), 256, 0, stream>>>(X, M, k, L32, LI32, Q);
+    chol_solve_kernel<NB><<<static_cast<unsigned>(ceil_div(M, kSolveRows)), 256, 0, stream>>>(X, M, k, L, LI, Q);
     BSQ_HIP(hipGetLastError());
 }
 
 template <int NB>
 void chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, const int *run, hipStream_t stream) {
     double *L = Lbuf, *LI = Lbuf + static_cast<uint64_t>(NB) * 32 * NB * 32;
-    chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, nullptr, nullptr, status, run);
+    chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, status, run);
     BSQ_HIP(hipGetLastError());
     trinv_kernel<NB><<<static_cast<unsigned>(ceil_div(k, 16)), kTrinvThreads, 0, stream>>>(L, LI, k, B, run);
     BSQ_HIP(hipGetLastError());
@@ -758,11 +760,10 @@ __global__ __launch_bounds__(256) void ns_refine_kernel(const double *__restrict
 }  // namespace
 
 // FP64 doubles needed by the L buffer of launch_chol_blocked and
-// launch_chol_solve for rank k: L and the diagonal-block inverses in FP64,
-// then the same two in FP32.
+// launch_chol_solve for rank k: L and the diagonal-block inverses.
 uint64_t chol_blocked_buffer_doubles(int k) {
-    const uint64_t nb = ceil_div(k, 32), d = nb * 32 * nb * 32 + nb * 1024;
-    return d + d / 2;
+    const uint64_t nb = ceil_div(k, 32);
+    return nb * 32 * nb * 32 + nb * 1024;
 }
 
 bool chol_blocked_supported(int k) { return k >= 1 && k <= 256; }
