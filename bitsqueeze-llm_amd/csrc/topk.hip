@@ -512,7 +512,6 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
 template <TopkSource SRC, int NV4>
 __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     __shared__ Shared sh;
-    __shared__ __attribute__((aligned(16))) unsigned long long tm[kThreads];
     __shared__ __attribute__((aligned(16))) unsigned long long bk[kFastCap];
     __shared__ float bv[kFastCap];
     const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
@@ -579,30 +578,41 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
             for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(v[m][u]));
         return t;
     };
-    bool nonzero = false;
-    unsigned long long tmax = 0;
-    uint32_t lt = lane_id();
+    // the lane's largest |v| (a compare-select skips NaN, which ranks lowest;
+    // all-NaN lanes keep -1), i.e. its largest 32-bit order key
+    float mx = -1.0f;
 #pragma unroll
-    for (int m = 0; m < NV4; ++m) {
+    for (int m = 0; m < NV4; ++m)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            nonzero |= fabsf(v[m][u]) > FLT_EPSILON;  // false for the NaN padding
-            const unsigned long long K = key_of(lt, m, u);
-            tmax = K > tmax ? K : tmax;
+            const float f = fabsf(v[m][u]);
+            mx = f > mx ? f : mx;
         }
-        __builtin_amdgcn_sched_barrier(0);  // keep each quad's keys short-lived
-    }
+    const uint32_t key32 = mx >= 0.0f ? __float_as_uint(mx) + 1u : 0u;
+    const bool nonzero = mx > FLT_EPSILON;  // false for NaN-only and padding lanes
     if (a.flags && __syncthreads_or(nonzero ? 1 : 0)) {
         if (tid == 0) atomicOr(a.flags, kFlagError);
     }
-    tm[tid] = tmax;
-    __syncthreads();
-    // lanes with columns have distinct maxima; k <= those lanes
-    if (count_greater(tm, kThreads, tmax) == k - 1) sh.kt = tmax;
-    __syncthreads();
-    unsigned long long kt = sh.kt;
-    // candidates by magnitude (a superset of the keys >= kt, ranked exactly
-    // below); a NaN threshold takes the radix path
+    // filter threshold: the top 16 bits of the k-th largest lane maximum's
+    // order key, by two 8-bit radix passes over one key per lane (k lanes
+    // hold a key >= it, so at least k entries pass; the candidates are then
+    // ranked exactly, so any such lower bound gives the same result)
+    uint32_t prefix = 0, remaining = k;
+#pragma unroll
+    for (int shift = 24; shift >= 16; shift -= 8) {
+        sh.hist[tid] = 0;
+        __syncthreads();
+        const uint32_t hmask = shift == 24 ? 0u : 0xFF000000u;
+        if ((key32 & hmask) == prefix) atomicAdd(&sh.hist[(key32 >> shift) & 255u], 1u);
+        __syncthreads();
+        choose_digit(sh, remaining);
+        prefix |= sh.digit << shift;
+        remaining -= sh.above;
+    }
+    unsigned long long kt = static_cast<unsigned long long>(prefix) << 16;
+    uint32_t lt;
+    // candidates by magnitude (a superset of the top k, ranked exactly
+    // below); a threshold without a number takes the radix path
     const bool kt_number = (kt >> 16) != 0;
     const MagThreshold th(kt_number ? kt : (1ull << 16));
     uint32_t cnt = 0;
