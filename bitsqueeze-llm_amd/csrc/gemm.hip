@@ -15,16 +15,20 @@
 //
 // Tiling: 256 threads = 4 waves in a 2 x 2 grid; workgroup tile 128 x 128,
 // BK = 16; each wave owns 64 x 64 as 4 x 4 MFMA 16x16 blocks (64 AGPRs).
-// Two main loops share that tiling:
-//   gemm_dma_kernel   operand tiles go global -> LDS directly
-//                     (global_load_lds_dwordx4) through a ring of four
-//                     slices, three in flight while one is multiplied;
-//   gemm_mfma_kernel  the fallback for shapes the DMA layout does not take
-//                     (K not a multiple of 16, unaligned operands): tiles move
-//                     global -> registers -> LDS one slice ahead.
-// Both use the same k order per lane, so their results are identical.  Skinny shapes are split
-// along K so the grid fills the 256 CUs several times over; partial products
-// go to a workspace summed in a fixed order, so results are deterministic.
+// Three main loops share that tiling:
+//   gemm_dma_kernel     operand tiles go global -> LDS directly
+//                       (global_load_lds_dwordx4) through a ring of four
+//                       slices, three in flight while one is multiplied;
+//   gemm_streamk_kernel the same ring in a persistent grid that splits
+//                       tiles x K slices evenly over two workgroups per CU;
+//   gemm_mfma_kernel    the fallback for shapes the DMA layout does not take
+//                       (K not a multiple of 16, unaligned operands): tiles
+//                       move global -> registers -> LDS one slice ahead.
+// All use the same k order per lane, so for the same K partition their
+// results are identical.  Skinny shapes are split along K so the grid fills
+// the 256 CUs several times over (stream-K on the DMA path when the split
+// grid is not a whole number of rounds); partial products go to a workspace
+// summed in a fixed order, so results are deterministic.
 #include "bsq_internal.hpp"
 #include "tile_map.hpp"
 
@@ -587,6 +591,213 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
             }
 }
 
+// ---------------------------------------------------------------------------
+// Stream-K form of the DMA-pipelined kernel for the long-K, few-tile products
+// of the range finder (n x q outputs, K = m or n).  A persistent grid of G
+// workgroups (two per CU) splits the flattened space of tiles x K slices, in
+// pairs of slices, into G equal contiguous ranges, so every CU does the same
+// work whatever the tile count, and each workgroup fills its DMA ring once:
+// the ring runs on across tile boundaries, and the partial tile that ends at
+// a boundary is written out while the next tile's slices are already in
+// flight.  Logical workgroup L (pair ranges [L P / G, (L + 1) P / G), P =
+// tiles x slices / 2) is placed so that each XCD runs a contiguous eighth of
+// the space (a few A panels).  Each workgroup writes the partial tile of every
+// tile it touches to slot (tile, L - first owner) and streamk_reduce_kernel
+// sums each tile's slots in that fixed order, so results are deterministic.
+// Needs an even number of slices per tile (tile boundaries then fall between
+// pairs, after the second or fourth slice of an unrolled group of four).
+struct StreamK {
+    float *ws;     // partial tiles [tile][part][128][128]
+    int tiles_n;   // output tiles per row of tiles
+    int nk;        // K slices per tile (even)
+    int pairs;     // tiles x nk / 2
+    int maxparts;  // workspace slots per tile
+};
+
+// logical workgroup whose range holds slice pair `pr`
+__host__ __device__ __forceinline__ int sk_owner(int64_t pr, int64_t pairs, int G) {
+    return static_cast<int>(((pr + 1) * G - 1) / pairs);
+}
+
+// (two waves per SIMD requested explicitly: left to itself the register
+// allocator splits the accumulators between AGPRs and VGPRs around the
+// partial-tile writes and needs more than half the register file)
+template <bool TA, bool TB>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_streamk_kernel(
+    GemmArgs g, StreamK sk) {
+    constexpr int T = 128, BM = T, BN = T;
+    constexpr int kTileF = T * BK;
+    constexpr int kStageF = 2 * kTileF;
+    constexpr int kChunks = T / 16;
+    constexpr int kCpw = kChunks / 4;
+    constexpr int kDmaPerSlice = 2 * kCpw;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    __shared__ __attribute__((aligned(1024))) float st0[kStageF];
+    __shared__ __attribute__((aligned(1024))) float st1[kStageF];
+    __shared__ __attribute__((aligned(1024))) float st2[kStageF];
+    __shared__ __attribute__((aligned(1024))) float st3[kStageF];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    const int G = static_cast<int>(gridDim.x);
+    const int bid = static_cast<int>(blockIdx.x), xcd = bid % kXcds, loc = bid / kXcds;
+    const int L = xcd * (G / kXcds) + min(xcd, G % kXcds) + loc;
+    const int64_t pairs = sk.pairs;
+    const int p0 = static_cast<int>(static_cast<int64_t>(L) * pairs / G);
+    const int n = 2 * (static_cast<int>(static_cast<int64_t>(L + 1) * pairs / G) - p0);  // slices
+    const int it0 = 2 * p0;
+
+    f32x4v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+    // the next slice to issue, as running (tile row, tile column, slice)
+    const int tile0 = it0 / sk.nk;
+    int i_ks = it0 - tile0 * sk.nk;
+    int i_tm = tile0 / sk.tiles_n, i_tn = tile0 - i_tm * sk.tiles_n;
+    auto issue = [&](const float *st) {
+        const int m0 = i_tm * BM, n0 = i_tn * BN, k0 = i_ks * BK;
+#pragma unroll
+        for (int h = 0; h < kCpw; ++h) {
+            const int c = kCpw * wave + h;
+            dma_chunk<TA, T>(g.A, g.lda, m0, g.M, k0, c, st);
+            dma_chunk<!TB, T>(g.B, g.ldb, n0, g.N, k0, c, st + kTileF);
+        }
+        // advanced by selects: a branch here would split the MFMA chains
+        // across blocks and their accumulators across register classes
+        const bool wrap = i_ks + 1 == sk.nk;
+        i_ks = wrap ? 0 : i_ks + 1;
+        const int tn1 = i_tn + (wrap ? 1 : 0);
+        const bool wrap2 = tn1 == sk.tiles_n;
+        i_tn = wrap2 ? 0 : tn1;
+        i_tm += wrap2 ? 1 : 0;
+    };
+    const int kk = lane >> 4, cc = lane & 15;
+    // the tile being accumulated and its slices done so far
+    int c_tile = tile0, c_ks = it0 - tile0 * sk.nk;
+    // after the pair ending with local slice jl: at a tile's end or the range's
+    // end, the partial tile goes to its slot and the accumulators restart
+    auto pair_done = [&](int jl) {
+        c_ks += 2;
+        const bool tile_end = c_ks == sk.nk;
+        if (tile_end || jl + 1 == n) {  // uniform
+            const int first = sk_owner(static_cast<int64_t>(c_tile) * (sk.nk / 2), pairs, G);
+            float *W = sk.ws + (static_cast<uint64_t>(c_tile) * sk.maxparts + (L - first)) * (T * T);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        W[(wm0 + i * 16 + 4 * (lane >> 4) + r) * T + wn0 + j * 16 + (lane & 15)] = acc[i][j][r];
+                    acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+        c_ks = tile_end ? 0 : c_ks;
+        c_tile += tile_end ? 1 : 0;
+    };
+    // local slice j sits in stage j % 4: cur holds it, nxt (= stage (j + 3) % 4,
+    // read in iteration j - 1) receives local slice j + 3
+    auto body = [&](const float *cur, const float *nxt, int j) {
+        const int ahead = min(kStages - 2, n - 1 - j);
+        if (ahead >= 2) dma_barrier<2 * kDmaPerSlice>();
+        else if (ahead == 1) dma_barrier<kDmaPerSlice>();
+        else dma_barrier<0>();
+        if (j + kStages - 1 < n) issue(nxt);
+        float a[FM][KS], b[FN][KS];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) dma_frag<TA, T>(cur, wm0 + i * 16 + cc, kk, a[i]);
+#pragma unroll
+        for (int jj = 0; jj < FN; ++jj) dma_frag<!TB, T>(cur + kTileF, wn0 + jj * 16 + cc, kk, b[jj]);
+#pragma unroll
+        for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int jj = 0; jj < FN; ++jj)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s2], b[jj][s2], acc[i][jj], 0, 0, 0);
+    };
+    // steady state: every slice of the group has two slices issued behind
+    // the next one and issues its own successor three ahead
+    auto steady = [&](const float *cur, const float *nxt) {
+        dma_barrier<2 * kDmaPerSlice>();
+        issue(nxt);
+        float a[FM][KS], b[FN][KS];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) dma_frag<TA, T>(cur, wm0 + i * 16 + cc, kk, a[i]);
+#pragma unroll
+        for (int jj = 0; jj < FN; ++jj) dma_frag<!TB, T>(cur + kTileF, wn0 + jj * 16 + cc, kk, b[jj]);
+#pragma unroll
+        for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int jj = 0; jj < FN; ++jj)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s2], b[jj][s2], acc[i][jj], 0, 0, 0);
+    };
+    if (0 < n) issue(st0);
+    if (1 < n) issue(st1);
+    if (2 < n) issue(st2);
+    int j = 0;
+    for (; j + 2 * kStages <= n; j += kStages) {
+        steady(st0, st3);
+        steady(st1, st0);
+        pair_done(j + 1);
+        steady(st2, st1);
+        steady(st3, st2);
+        pair_done(j + 3);
+    }
+    for (; j < n; j += kStages) {  // the last two to six slices (n is even)
+        body(st0, st3, j);
+        body(st1, st0, j + 1);
+        pair_done(j + 1);
+        if (j + 2 < n) {
+            body(st2, st1, j + 2);
+            body(st3, st2, j + 3);
+            pair_done(j + 3);
+        }
+    }
+}
+
+// C = the sum of each tile's partial tiles in slot order.  One workgroup per
+// 16 rows of a tile, 16-byte accesses.
+__global__ __launch_bounds__(256) void streamk_reduce_kernel(StreamK sk, int G, int M, int N, int ldc,
+                                                             float *__restrict__ C) {
+    constexpr int T = 128;
+    const int tile = static_cast<int>(blockIdx.x) / (T / 16), rb = (static_cast<int>(blockIdx.x) % (T / 16)) * 16;
+    const int64_t pb = static_cast<int64_t>(tile) * (sk.nk / 2);
+    const int parts = sk_owner(pb + sk.nk / 2 - 1, sk.pairs, G) - sk_owner(pb, sk.pairs, G) + 1;
+    const int tm = tile / sk.tiles_n, tn = tile - tm * sk.tiles_n;
+    const bool vec = (ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & 15u) == 0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int lin = threadIdx.x + 256 * q, r = rb + lin / (T / 4), c4 = (lin % (T / 4)) * 4;
+        const float *W = sk.ws + static_cast<uint64_t>(tile) * sk.maxparts * (T * T) + r * T + c4;
+        float4 s = *reinterpret_cast<const float4 *>(W);
+        for (int p = 1; p < parts; ++p) {
+            const float4 v = *reinterpret_cast<const float4 *>(W + static_cast<uint64_t>(p) * (T * T));
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+        const int gi = tm * T + r, gj = tn * T + c4;
+        if (gi >= M) continue;
+        float *out = C + static_cast<uint64_t>(gi) * ldc + gj;
+        if (vec && gj + 4 <= N) {
+            *reinterpret_cast<float4 *>(out) = s;
+        } else {
+            const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (gj + u < N) out[u] = sv[u];
+        }
+    }
+}
+
 // C[i, j] = sum_z W[z][i, j] in a fixed order.
 __global__ void splitk_reduce_kernel(const float *__restrict__ W, int splits, uint64_t stride, int M, int N,
                                      int ldc, float *__restrict__ C) {
@@ -637,12 +848,49 @@ int choose_splits(int M, int N, int K) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Stream-K layout of a product that split-K would split (K a whole number of
+// slice pairs): G = two workgroups per CU, and the most owners any tile has.
+struct SkPlan {
+    bool on = false;
+    int G = 0;
+    StreamK sk{};
+    uint64_t bytes = 0;
+};
+SkPlan streamk_plan(int M, int N, int K) {
+    SkPlan p;
+    const int splits = choose_splits(M, N, K);
+    if (K % (2 * BK) != 0 || splits <= 1) return p;
+    const int tiles_n = static_cast<int>(ceil_div(N, 128));
+    const int tiles = static_cast<int>(ceil_div(M, 128)) * tiles_n;
+    // a split-K grid of whole rounds (two workgroups on every CU) is already
+    // balanced, and its fixed-order sum is the same; stream-K is for the rest
+    if ((static_cast<int64_t>(tiles) * splits) % (2 * static_cast<int64_t>(cu_count())) == 0) return p;
+    const int nk = K / BK;
+    const int64_t pairs = static_cast<int64_t>(tiles) * (nk / 2);
+    const int G = static_cast<int>(std::min<int64_t>(2 * static_cast<int64_t>(cu_count()), pairs));
+    int maxparts = 1;
+    for (int t = 0; t < tiles; ++t) {
+        const int64_t b = static_cast<int64_t>(t) * (nk / 2);
+        maxparts = std::max(maxparts, sk_owner(b + nk / 2 - 1, pairs, G) - sk_owner(b, pairs, G) + 1);
+    }
+    p.on = true;
+    p.G = G;
+    p.sk.tiles_n = tiles_n;
+    p.sk.nk = nk;
+    p.sk.pairs = static_cast<int>(pairs);
+    p.sk.maxparts = maxparts;
+    p.bytes = static_cast<uint64_t>(tiles) * maxparts * 128 * 128 * sizeof(float);
+    return p;
+}
+
 }  // namespace
 
-// Workspace bytes needed by launch_gemm for the given shape (split-K partials).
+// Workspace bytes needed by launch_gemm for the given shape (split-K partials
+// on the register-staged path, stream-K partial tiles on the DMA path).
 uint64_t gemm_workspace_bytes(int M, int N, int K) {
     const int splits = choose_splits(M, N, K);
-    return splits > 1 ? static_cast<uint64_t>(splits) * M * N * sizeof(float) : 0;
+    const uint64_t split_bytes = splits > 1 ? static_cast<uint64_t>(splits) * M * N * sizeof(float) : 0;
+    return std::max(split_bytes, streamk_plan(M, N, K).bytes);
 }
 
 void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda, const float *B, int ldb, float *C,
@@ -681,6 +929,28 @@ void launch_gemm(bool ta, bool tb, int M, int N, int K, const float *A, int lda,
     // register-staged one
     const bool dma = g.vec_a && g.vec_b && (K % BK == 0) && (!ta || M % 4 == 0) &&
                      (tb || N % 4 == 0) && (!recon || K <= kDmaReconMaxK);
+    // the long-K products in stream-K form
+    if (dma && !recon && splits > 1) {
+        SkPlan pl = streamk_plan(M, N, K);
+        if (pl.on && pl.bytes <= workspace_bytes) {
+            pl.sk.ws = workspace;
+            g.C = C;
+            g.ldc = ldc;
+            g.split_stride = 0;
+            g.splits = 1;
+            g.k_per_split = K;
+            const dim3 sgrid(static_cast<unsigned>(pl.G));
+            if (!ta && !tb) gemm_streamk_kernel<false, false><<<sgrid, kThreads, 0, stream>>>(g, pl.sk);
+            else if (ta && !tb) gemm_streamk_kernel<true, false><<<sgrid, kThreads, 0, stream>>>(g, pl.sk);
+            else if (!ta && tb) gemm_streamk_kernel<false, true><<<sgrid, kThreads, 0, stream>>>(g, pl.sk);
+            else gemm_streamk_kernel<true, true><<<sgrid, kThreads, 0, stream>>>(g, pl.sk);
+            BSQ_HIP(hipGetLastError());
+            const int tiles = static_cast<int>(ceil_div(M, 128) * ceil_div(N, 128));
+            streamk_reduce_kernel<<<static_cast<unsigned>(tiles * 8), 256, 0, stream>>>(pl.sk, pl.G, M, N, ldc, C);
+            BSQ_HIP(hipGetLastError());
+            return;
+        }
+    }
     // 64 x 64 tiles when 128 x 128 ones (unsplit) would not give every CU two
     // workgroups: the short-K products of the orthonormalisation
     const bool t64 = dma && !recon && splits == 1 &&
