@@ -461,14 +461,13 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
         }
     };
     const int kk = lane >> 4, cc = lane & 15;
-    // RECON: the minuend of the output tile (four 32-row passes of Q float4
-    // per thread) is requested right after the last operand slice, so it
-    // arrives while the last slices are multiplied.  Every lane issues all
-    // kMv loads (addresses clamped into the matrix), so the waits below can
-    // count them.
-    constexpr int Q = 32 * BN / 4 / kThreads;
-    constexpr int kMv = RECON ? 4 * Q : 0;
-    float4 mvall[4][Q];
+    // RECON: the minuend of this wave's 64 x 64 output block (16 float4 per
+    // lane, in the layout the epilogue stores) is requested right after the
+    // last operand slice, so it arrives while the last slices are multiplied.
+    // Every lane issues all kMv loads (addresses clamped into the matrix), so
+    // the waits below can count them.
+    constexpr int kMv = RECON ? WM * WN / 4 / 64 : 0;
+    float4 mvall[RECON ? kMv : 1];
     const bool vec_c = RECON && ((g.ldc & 3) == 0) &&
                        ((reinterpret_cast<uintptr_t>(g.C + static_cast<uint64_t>(zs) * g.split_stride) & 15u) == 0) &&
                        (!g.minuend || (reinterpret_cast<uintptr_t>(g.minuend) & 15u) == 0);
@@ -476,13 +475,10 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
     auto issue_minuend = [&]() {
         asm volatile("" ::: "memory");  // stays behind the last slice's DMA
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-            for (int q = 0; q < Q; ++q) {
-                const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
-                const int gi = min(m0 + 32 * p + rr, g.M - 1), gj = min(n0 + 4 * c4, g.N - 4);
-                mvall[p][q] = *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj);
-            }
+        for (int q = 0; q < kMv; ++q) {
+            const int gi = min(m0 + wm0 + 4 * q + (lane >> 4), g.M - 1), gj = min(n0 + wn0 + 4 * (lane & 15), g.N - 4);
+            mvall[q] = *reinterpret_cast<const float4 *>(g.minuend + static_cast<uint64_t>(gi) * g.ldc + gj);
+        }
         asm volatile("" ::: "memory");
     };
     // slice j sits in stage j % 4: cur holds it, nxt (= stage (j + 3) % 4, read
@@ -537,44 +533,37 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
     float *C = g.C + static_cast<uint64_t>(zs) * g.split_stride;
     // fragment (i, j) register r holds row 4*(lane/16) + r, column lane % 16
     if constexpr (RECON) {
-        // the output tile leaves through stage 0 in four 32-row passes so that
-        // rows go out as 16-byte stores and the minuend comes in as 16-byte
-        // loads; columns are XOR-swizzled by 16 on alternate groups of four
-        // rows (the fragment writes of rows r and r + 4 then hit disjoint banks)
-        float *Cs = st0;
+        // every wave leaves with its own 64 x 64 block through its own 16 KB
+        // of the ring, after one barrier (the ring is consumed): rows go out
+        // as 16-byte stores, the minuend comes in as 16-byte loads; columns
+        // are XOR-swizzled by 16 on alternate groups of four rows (the
+        // fragment writes of rows r and r + 4 then hit disjoint banks)
+        __syncthreads();
+        float *Cw = wave == 0 ? st0 : (wave == 1 ? st1 : (wave == 2 ? st2 : st3));
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const float4(&mv)[Q] = mvall[p];
-            __syncthreads();  // the ring (p = 0) or the previous pass is consumed
-            if (wm0 == 64 * (p / 2)) {
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int ii = 0; ii < 2; ++ii)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
-                    for (int j = 0; j < FN; ++j)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int rl = 16 * ii + 4 * (lane >> 4) + r;
-                            const int col = wn0 + j * 16 + (lane & 15);
-                            Cs[rl * BN + (col ^ (16 * ((rl >> 2) & 1)))] = acc[2 * (p % 2) + ii][j][r];
-                        }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int q = 0; q < Q; ++q) {
-                const int lin = tid + q * kThreads, rr = lin / (BN / 4), c4 = lin % (BN / 4);
-                const int gi = m0 + 32 * p + rr, gj = n0 + 4 * c4;
-                if (gi >= g.M) continue;
-                float4 v = *reinterpret_cast<const float4 *>(&Cs[rr * BN + ((4 * c4) ^ (16 * ((rr >> 2) & 1)))]);
-                const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
-                if (vec_c && gj + 4 <= g.N) {
-                    if (mv_on) v = float4{mv[q].x - v.x, mv[q].y - v.y, mv[q].z - v.z, mv[q].w - v.w};
-                    *reinterpret_cast<float4 *>(C + e) = v;
-                } else {
-                    const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        if (gj + u < g.N) C[e + u] = g.minuend ? g.minuend[e + u] - vv[u] : vv[u];
+                for (int r = 0; r < 4; ++r) {
+                    const int rl = 16 * i + 4 * (lane >> 4) + r, col = 16 * j + (lane & 15);
+                    Cw[rl * WN + (col ^ (16 * ((rl >> 2) & 1)))] = acc[i][j][r];
                 }
+#pragma unroll
+        for (int q = 0; q < kMv; ++q) {
+            const int rl = 4 * q + (lane >> 4), c4 = 4 * (lane & 15);
+            const int gi = m0 + wm0 + rl, gj = n0 + wn0 + c4;
+            if (gi >= g.M) continue;
+            float4 v = *reinterpret_cast<const float4 *>(&Cw[rl * WN + (c4 ^ (16 * ((rl >> 2) & 1)))]);
+            const uint64_t e = static_cast<uint64_t>(gi) * g.ldc + gj;
+            if (vec_c && gj + 4 <= g.N) {
+                if (mv_on) v = float4{mvall[q].x - v.x, mvall[q].y - v.y, mvall[q].z - v.z, mvall[q].w - v.w};
+                *reinterpret_cast<float4 *>(C + e) = v;
+            } else {
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (gj + u < g.N) C[e + u] = g.minuend ? g.minuend[e + u] - vv[u] : vv[u];
             }
         }
         return;

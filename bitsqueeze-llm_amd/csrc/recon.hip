@@ -67,8 +67,8 @@ __device__ __forceinline__ float guarded_dq(const float *p) {
 // LDS layout of one workgroup (bytes): codes of the tile's U rows and V rows
 // (row pitch K/2 + 16: 16-byte aligned rows that start four banks apart),
 // their block scales as floats, S, and the table of level pairs
-// L2[b] = (L[b >> 4], L[b & 15]).  The epilogue's 32 x 128 staging of the
-// output reuses the start of the block.
+// L2[b] = (L[b >> 4], L[b & 15]).  The epilogue's staging of the output
+// (32 x 64 floats per wave) reuses the start of the block.
 struct Layout {
     int pitch, cA, cB, sA, sB, sv, l2, bytes;
     __host__ __device__ explicit Layout(int K) {
@@ -80,7 +80,7 @@ struct Layout {
         sv = sB + TT * (K / 64) * 4;
         l2 = sv + K * 4;
         bytes = l2 + 256 * 8;
-        if (bytes < 32 * TT * 4) bytes = 32 * TT * 4;
+        if (bytes < 4 * 32 * 64 * 4) bytes = 4 * 32 * 64 * 4;
     }
 };
 
@@ -173,33 +173,30 @@ __global__ __launch_bounds__(kThreads) void recon_q_kernel(ReconQArgs g) {
                     acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s2], b[jj][s2], acc[i][jj], 0, 0, 0);
     }
 
-    // epilogue: the tile leaves through LDS in four 32-row passes (16-byte
-    // stores; columns XOR-swizzled by 16 on alternate groups of four rows)
-    constexpr int Q = 32 * TT / 4 / kThreads;
+    // epilogue: every wave leaves with its own 64 x 64 block through its own
+    // 8 KB of LDS in two 32-row passes (16-byte stores; columns XOR-swizzled
+    // by 16 on alternate groups of four rows), after one barrier (the codes
+    // are consumed)
     const bool vec_out = ((g.N & 3) == 0) && ((reinterpret_cast<uintptr_t>(g.out) & 15u) == 0);
-    float *Cs = reinterpret_cast<float *>(smem);
+    __syncthreads();
+    float *Cw = reinterpret_cast<float *>(smem) + wave * (32 * 64);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        __syncthreads();  // the codes (p = 0) or the previous pass are consumed
-        if (wm0 == 64 * (p / 2)) {
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
+        for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
+            for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int rl = 16 * ii + 4 * (lane >> 4) + r;
-                        const int col = wn0 + jj * 16 + (lane & 15);
-                        Cs[rl * TT + (col ^ (16 * ((rl >> 2) & 1)))] = acc[2 * (p % 2) + ii][jj][r];
-                    }
-        }
-        __syncthreads();
+                for (int r = 0; r < 4; ++r) {
+                    const int rl = 16 * ii + 4 * (lane >> 4) + r, col = 16 * jj + (lane & 15);
+                    Cw[rl * 64 + (col ^ (16 * ((rl >> 2) & 1)))] = acc[2 * h + ii][jj][r];
+                }
 #pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            const int lin = tid + q * kThreads, rr = lin / (TT / 4), c4 = lin % (TT / 4);
-            const int gi = m0 + 32 * p + rr, gj = n0 + 4 * c4;
+        for (int q = 0; q < 8; ++q) {
+            const int rl = 4 * q + (lane >> 4), c4 = 4 * (lane & 15);
+            const int gi = m0 + wm0 + 32 * h + rl, gj = n0 + wn0 + c4;
             if (gi >= g.M) continue;
-            const float4 v = *reinterpret_cast<const float4 *>(&Cs[rr * TT + ((4 * c4) ^ (16 * ((rr >> 2) & 1)))]);
+            const float4 v = *reinterpret_cast<const float4 *>(&Cw[rl * 64 + (c4 ^ (16 * ((rl >> 2) & 1)))]);
             const uint64_t e = static_cast<uint64_t>(gi) * g.N + gj;
             if (vec_out && gj + 4 <= g.N) {
                 *reinterpret_cast<float4 *>(g.out + e) = v;
