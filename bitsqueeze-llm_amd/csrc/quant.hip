@@ -57,8 +57,7 @@ __device__ __noinline__ uint32_t nf4_code_scan(float v) {
 // 15 and 0).  |v| >= 2 and non-finite v take the scan.  Exhaustively
 // checked against the scan over all 2^32 floats by the GPU test suite.
 struct Nf4Table {
-    float thr[256];
-    uint32_t lo[256];
+    uint2 ent[256];  // (bits of the threshold inside bin b, code_lo): one 8-byte read
 };
 
 __device__ __forceinline__ void nf4_table_build(Nf4Table &t) {
@@ -72,16 +71,19 @@ __device__ __forceinline__ void nf4_table_build(Nf4Table &t) {
             lo += (T[i] <= e0) ? 1u : 0u;
             if (T[i] > e0 && T[i] < e1) thr = T[i];
         }
-        t.thr[b] = thr;
-        t.lo[b] = lo;
+        t.ent[b] = uint2{__float_as_uint(thr), lo};
     }
 }
 
+// the table path alone: |v| < 2
+__device__ __forceinline__ uint32_t nf4_code_small(const Nf4Table &t, float v) {
+    const int b = min(max(static_cast<int>((v + 1.0f) * 128.0f), 0), 255);
+    const uint2 e = t.ent[b];
+    return e.y + ((v >= __uint_as_float(e.x)) ? 1u : 0u);
+}
+
 __device__ __forceinline__ uint32_t nf4_code(const Nf4Table &t, float v) {
-    if (fabsf(v) < 2.0f) {
-        const int b = min(max(static_cast<int>((v + 1.0f) * 128.0f), 0), 255);
-        return t.lo[b] + ((v >= t.thr[b]) ? 1u : 0u);
-    }
+    if (fabsf(v) < 2.0f) return nf4_code_small(t, v);
     return nf4_code_scan(v);
 }
 
@@ -145,15 +147,20 @@ __device__ __forceinline__ float dq_effective(float dq) {
 // aligned group of 8 lanes and the per-block scale work is shared by 8 lanes.
 // Each thread takes kUnroll chunks per loop iteration, their loads issued
 // together before any is used (one chunk per iteration left these kernels
-// latency-bound).
-constexpr int kUnroll = 4;
+// latency-bound); the encoder also issues the next iteration's loads before
+// encoding the current one (two chunks per iteration measured best with
+// that: four take 144 VGPRs, three waves per SIMD).
+constexpr int kUnroll = 2;
 
 // Pass 1 of NF4_DQ: max over blocks of the block scale (absmax, or 1 for an
-// all-zero block), accumulated as float bits (all values >= 0) with one
-// atomicMax per workgroup.  Replaces compute_block_absmax_kernel +
-// cub::DeviceReduce::Max (quantization_cuda.cu:186-220, 594-602).
+// all-zero block), as float bits (all values >= 0): each workgroup writes
+// its maximum to out[blockIdx.x] (PARTIAL; rows_gmax_kernel reduces those)
+// or takes it into out[0] with atomicMax.  Replaces
+// compute_block_absmax_kernel + cub::DeviceReduce::Max
+// (quantization_cuda.cu:186-220, 594-602).
+template <bool PARTIAL>
 __global__ __launch_bounds__(kThreads) void dq_gmax_kernel(const float *__restrict__ x, uint64_t n,
-                                                            bool vec_ok, uint32_t *__restrict__ gmax) {
+                                                            bool vec_ok, uint32_t *__restrict__ out) {
     const uint64_t nchunks = ceil_div(n, 8), nblocks = ceil_div(n, kQuantBlock);
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
     float local = 0.0f;
@@ -185,7 +192,8 @@ __global__ __launch_bounds__(kThreads) void dq_gmax_kernel(const float *__restri
     if (threadIdx.x == 0) {
         float m = wmax[0];
         for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, wmax[w]);
-        atomicMax(gmax, __float_as_uint(m));
+        if constexpr (PARTIAL) out[blockIdx.x] = __float_as_uint(m);
+        else atomicMax(out, __float_as_uint(m));
     }
 }
 
@@ -205,8 +213,10 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
         if (blockIdx.x == 0 && threadIdx.x == 0) *dq_out = raw;
     }
     __syncthreads();
-    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads; base < nchunks; base += kUnroll * stride) {
-        float v[kUnroll][8];
+    // chunks of one iteration: loaded one iteration ahead (two register
+    // sets), so the loads of iteration i + 1 are in flight while iteration i
+    // is encoded
+    auto load_it = [&](uint64_t base, float (&v)[kUnroll][8]) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const uint64_t chunk = base + u * stride + threadIdx.x;
@@ -215,6 +225,8 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[u][i] = 0.0f;
         }
+    };
+    auto encode_it = [&](uint64_t base, float (&v)[kUnroll][8]) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const uint64_t chunk = base + u * stride + threadIdx.x;
@@ -241,13 +253,39 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
                 else scales_f32[chunk / 8] = scale;
             }
             if (valid) {
+                // |v inv| < 2 (the table) unless a block scale fell far below
+                // the block's absmax (an NF4_DQ scale code of 0 replaced by 1):
+                // one test per chunk, the scan only for such chunks
+                float w[8];
+                bool small = true;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    w[i] = v[u][i] * inv;
+                    small = small && (fabsf(w[i]) < 2.0f);
+                }
                 uint32_t c[8];
                 const uint64_t e0 = chunk * 8;
+                if (small) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code(tab, v[u][i] * inv) : 0u;  // odd tail: low nibble 0
+                    for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code_small(tab, w[i]) : 0u;  // odd tail: low nibble 0
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code(tab, w[i]) : 0u;
+                }
                 store_codes(codes, n, chunk, vec_ok, c);
             }
         }
+    };
+    const uint64_t step = static_cast<uint64_t>(kUnroll) * stride;
+    float va[kUnroll][8], vb[kUnroll][8];
+    uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads;
+    if (base < nchunks) load_it(base, va);
+    for (; base < nchunks; base += 2 * step) {  // uniform
+        if (base + step < nchunks) load_it(base + step, vb);
+        encode_it(base, va);
+        if (base + step >= nchunks) break;
+        if (base + 2 * step < nchunks) load_it(base + 2 * step, va);
+        encode_it(base + step, vb);
     }
 }
 
@@ -361,6 +399,18 @@ __global__ __launch_bounds__(kThreads) void nf4_code_sweep_kernel(uint64_t lo, u
     atomicAdd(checksum, cs);
 }
 
+// *gmax = bits of max_r row_gmax[r] (one workgroup; max is order-free).
+__global__ __launch_bounds__(kThreads) void rows_gmax_kernel(const float *__restrict__ row_gmax, uint32_t rows,
+                                                             uint32_t *__restrict__ gmax) {
+    __shared__ float red[kThreads / 64];
+    float m = 0.0f;
+    for (uint32_t i = threadIdx.x; i < rows; i += kThreads) m = fmaxf(m, row_gmax[i]);
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) *gmax = __float_as_uint(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+
 unsigned grid_for(uint64_t work_items, unsigned per_cu = 8) {
     const uint64_t want = ceil_div(work_items, kThreads);
     const uint64_t cap = static_cast<uint64_t>(cu_count()) * per_cu;
@@ -384,10 +434,21 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
                                                                   nullptr, codes);
     } else if (method == kMethodNF4DQ) {
         BSQ_REQUIRE(scales_u8 && codes && dq_out && gmax_scratch, "quant encode: null NF4_DQ output");
-        BSQ_HIP(hipMemsetAsync(gmax_scratch, 0, sizeof(uint32_t), stream));
-        // one workgroup per CU: every workgroup ends in one device-scope
-        // atomic on the same word, and those serialise across the XCDs
-        dq_gmax_kernel<<<grid_for(ceil_div(n, 8), 1), kThreads, 0, stream>>>(x, n, vec_ok, gmax_scratch);
+        // the workgroup maxima go to the start of the code buffer, which the
+        // encode below overwrites (ceil(n / 2) bytes hold 4 bytes for each of
+        // the at most n / 2048 workgroups), and one workgroup reduces them:
+        // no allocation, and no device-scope atomics on one word (those
+        // serialise across the XCDs, which held this pass to one workgroup
+        // per CU and ~4 TB/s)
+        uint32_t *partial = reinterpret_cast<uint32_t *>(codes);
+        if ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0 && 4ull * grid <= ceil_div(n, 2)) {
+            dq_gmax_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, partial);
+            rows_gmax_kernel<<<1, kThreads, 0, stream>>>(reinterpret_cast<const float *>(partial), grid,
+                                                         gmax_scratch);
+        } else {  // a code buffer that cannot hold aligned words: one workgroup per CU, atomics
+            BSQ_HIP(hipMemsetAsync(gmax_scratch, 0, sizeof(uint32_t), stream));
+            dq_gmax_kernel<false><<<grid_for(ceil_div(n, 8), 1), kThreads, 0, stream>>>(x, n, vec_ok, gmax_scratch);
+        }
         quant_encode_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8, gmax_scratch,
                                                                  dq_out, codes);
     } else {
@@ -396,19 +457,6 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
     BSQ_HIP(hipGetLastError());
 }
 
-namespace {
-// *gmax = bits of max_r row_gmax[r] (one workgroup; max is order-free).
-__global__ __launch_bounds__(kThreads) void rows_gmax_kernel(const float *__restrict__ row_gmax, uint32_t rows,
-                                                             uint32_t *__restrict__ gmax) {
-    __shared__ float red[kThreads / 64];
-    float m = 0.0f;
-    for (uint32_t i = threadIdx.x; i < rows; i += kThreads) m = fmaxf(m, row_gmax[i]);
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) *gmax = __float_as_uint(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-}
-}  // namespace
 
 void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gmax, uint32_t rows,
                                  uint8_t *scales_u8, float *dq_out, uint8_t *codes, uint32_t *gmax_scratch,
