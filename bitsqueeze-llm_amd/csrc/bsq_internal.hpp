@@ -93,6 +93,18 @@ void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gm
 void launch_quant_decode(uint64_t n, int method, const float *scales_f32,
                          const uint8_t *scales_u8, const float *dq, const uint8_t *codes,
                          float *out, hipStream_t stream);
+// Decode of a rows x cols direct section fused with the decompress's top-k
+// scatter (error set idx0 / val0 gated by *gate0's error flag when gate0 is
+// given, then the outlier set idx1 / val1; k per row, in-row indices, those
+// >= cols skipped): the same bytes as launch_quant_decode followed by
+// launch_topk_scatter, one workgroup and one LDS row per matrix row.
+constexpr uint32_t kDecodeRowsMaxCols = 32768;
+bool quant_decode_rows_supported(uint32_t rows, uint32_t cols);
+void launch_quant_decode_rows(uint32_t rows, uint32_t cols, int method, const float *scales_f32,
+                              const uint8_t *scales_u8, const float *dq, const uint8_t *codes,
+                              const uint16_t *idx0, const float *val0, uint32_t k0, const uint32_t *gate0,
+                              const uint16_t *idx1, const float *val1, uint32_t k1, float *out,
+                              hipStream_t stream);
 void launch_nf4_code_batch(const float *v, uint64_t n, uint8_t *codes, hipStream_t stream);
 void launch_e4m3_encode_batch(const float *v, uint64_t n, uint8_t *codes, hipStream_t stream);
 void launch_e4m3_decode_batch(const uint8_t *c, uint64_t n, float *v, hipStream_t stream);

@@ -351,6 +351,97 @@ __global__ __launch_bounds__(kThreads) void quant_decode_kernel(
     }
 }
 
+// Decode of a direct section fused with the top-k scatter of the decompress
+// (quantization_cuda.cu:287-341, then topk_cuda_utils.cuh:132-149 for the
+// error set and the outlier set, src/bitsqz_llm.cu:1373-1387): one
+// workgroup per row decodes the row into LDS, adds the error set (when the
+// gate word has the error flag) and then the outlier set there (indices >=
+// cols skipped, as the separate scatter does), and stores the row once.
+// Each element gets fl(fl(decoded + error) + outlier), as from decode +
+// scatter, without the scatter's read-modify-write pass over the matrix.
+// The row's top-k entries are requested before the codes are decoded.
+constexpr int kRowThreads = 512;  // eight waves per row: the LDS row limits workgroups per CU
+
+template <bool DQ>
+__global__ __launch_bounds__(kRowThreads) void quant_decode_rows_kernel(
+    uint32_t cols, bool vec_ok, const float *__restrict__ scales_f32, const uint8_t *__restrict__ scales_u8,
+    const float *__restrict__ dq_ptr, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ idx0,
+    const float *__restrict__ val0, uint32_t k0, const uint32_t *__restrict__ gate0,
+    const uint16_t *__restrict__ idx1, const float *__restrict__ val1, uint32_t k1, float *__restrict__ out) {
+    constexpr float Lc[16] = BSQ_NF4_LEVELS;
+    __shared__ float L[16];
+    extern __shared__ __attribute__((aligned(16))) float row[];
+    const uint32_t t = threadIdx.x;
+    const uint64_t r = blockIdx.x, e0 = r * cols;
+    if (t < 16) L[t] = Lc[t];
+    // first entries of both sets (the common case k <= 512: all of them)
+    if (gate0 && !(*gate0 & kFlagError)) k0 = 0;
+    uint32_t c0 = 0xFFFFFFFFu, c1 = 0xFFFFFFFFu;
+    float v0 = 0.0f, v1 = 0.0f;
+    if (t < k0) {
+        c0 = idx0[r * k0 + t];
+        v0 = val0[r * k0 + t];
+    }
+    if (t < k1) {
+        c1 = idx1[r * k1 + t];
+        v1 = val1[r * k1 + t];
+    }
+    float dq = 1.0f;
+    if constexpr (DQ) dq = dq_effective(*dq_ptr);
+    auto scale_of = [&](uint64_t b) {
+        float s;
+        if constexpr (DQ) s = dq * e4m3_decode(scales_u8[b]);
+        else s = scales_f32[b];
+        return (s == 0.0f || !__builtin_isfinite(s)) ? 1.0f : s;
+    };
+    __syncthreads();  // L
+    if (vec_ok) {
+        // 16 elements (8 code bytes, one block scale) per lane per step
+        for (uint32_t i = 16 * t; i < cols; i += 16 * kRowThreads) {
+            const uint64_t e = e0 + i;
+            const uint2 w = *reinterpret_cast<const uint2 *>(codes + e / 2);
+            const float s = scale_of(e / kQuantBlock);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t word = h ? w.y : w.x;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const uint32_t b0 = (word >> (16 * q)) & 0xFFu, b1 = (word >> (16 * q + 8)) & 0xFFu;
+                    *reinterpret_cast<float4 *>(row + i + 8 * h + 4 * q) =
+                        float4{s * L[b0 >> 4], s * L[b0 & 15u], s * L[b1 >> 4], s * L[b1 & 15u]};
+                }
+            }
+        }
+    } else {
+        for (uint32_t i = t; i < cols; i += kRowThreads) {
+            const uint64_t e = e0 + i;
+            const uint8_t byte = codes[e >> 1];
+            const uint32_t code = (e & 1) ? (byte & 15u) : (byte >> 4);
+            row[i] = scale_of(e / kQuantBlock) * L[code];
+        }
+    }
+    __syncthreads();
+    if (c0 < cols) row[c0] += v0;
+    for (uint32_t j = t + kRowThreads; j < k0; j += kRowThreads) {
+        const uint32_t c = idx0[r * k0 + j];
+        if (c < cols) row[c] += val0[r * k0 + j];
+    }
+    __syncthreads();  // the error set lands before the outlier set
+    if (c1 < cols) row[c1] += v1;
+    for (uint32_t j = t + kRowThreads; j < k1; j += kRowThreads) {
+        const uint32_t c = idx1[r * k1 + j];
+        if (c < cols) row[c] += val1[r * k1 + j];
+    }
+    __syncthreads();
+    if (vec_ok) {
+        float4 *o = reinterpret_cast<float4 *>(out + e0);
+        const float4 *src = reinterpret_cast<const float4 *>(row);
+        for (uint32_t i = t; i < cols / 4; i += kRowThreads) o[i] = src[i];
+    } else {
+        for (uint32_t i = t; i < cols; i += kRowThreads) out[e0 + i] = row[i];
+    }
+}
+
 __global__ void nf4_code_batch_kernel(const float *__restrict__ v, uint64_t n, uint8_t *__restrict__ c) {
     __shared__ Nf4Table tab;
     nf4_table_build(tab);
@@ -485,6 +576,39 @@ void launch_quant_decode(uint64_t n, int method, const float *scales_f32, const 
         quant_decode_kernel<true><<<grid, kThreads, 0, stream>>>(n, vec_ok, nullptr, scales_u8, dq, codes, out);
     } else {
         fail("quant decode: unsupported method");
+    }
+    BSQ_HIP(hipGetLastError());
+}
+
+bool quant_decode_rows_supported(uint32_t rows, uint32_t cols) {
+    return rows > 0 && cols > 0 && cols <= kDecodeRowsMaxCols;
+}
+
+void launch_quant_decode_rows(uint32_t rows, uint32_t cols, int method, const float *scales_f32,
+                              const uint8_t *scales_u8, const float *dq, const uint8_t *codes,
+                              const uint16_t *idx0, const float *val0, uint32_t k0, const uint32_t *gate0,
+                              const uint16_t *idx1, const float *val1, uint32_t k1, float *out,
+                              hipStream_t stream) {
+    BSQ_REQUIRE(quant_decode_rows_supported(rows, cols) && codes && out, "row decode: bad arguments");
+    BSQ_REQUIRE((k0 == 0 || (idx0 && val0)) && (k1 == 0 || (idx1 && val1)), "row decode: null top-k list");
+    // 16-element steps: rows start on 16 elements, 8-byte code and 16-byte
+    // output alignment
+    const bool vec_ok = cols % 16 == 0 && ((reinterpret_cast<uintptr_t>(codes) & 7u) == 0) && aligned16(out);
+    const size_t lds = static_cast<size_t>(cols) * sizeof(float);
+    auto go = [&](auto kern) {
+        BSQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(lds)));
+        kern<<<rows, kRowThreads, lds, stream>>>(cols, vec_ok, scales_f32, scales_u8, dq, codes, idx0, val0, k0, gate0,
+                                              idx1, val1, k1, out);
+    };
+    if (method == kMethodNF4) {
+        BSQ_REQUIRE(scales_f32, "row decode: null NF4 scales");
+        go(quant_decode_rows_kernel<false>);
+    } else if (method == kMethodNF4DQ) {
+        BSQ_REQUIRE(scales_u8 && dq, "row decode: null NF4_DQ scales");
+        go(quant_decode_rows_kernel<true>);
+    } else {
+        fail("row decode: unsupported method");
     }
     BSQ_HIP(hipGetLastError());
 }

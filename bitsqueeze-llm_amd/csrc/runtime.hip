@@ -639,6 +639,13 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
         const uint64_t N = static_cast<uint64_t>(rows) * cols;
         if (P.d_dense[SEC_DIRECT]) {
             BSQ_HIP(hipMemcpyAsync(d_dst, P.d_dense[SEC_DIRECT], N * 4, hipMemcpyDeviceToDevice, st));
+        } else if (scatter && (ke > 0 || ko > 0) && quant_decode_rows_supported(rows, cols)) {
+            // decode and both top-k sets in one pass over the rows
+            launch_quant_decode_rows(rows, cols, H.quantization_only_format, P.d_scales_f32[SEC_DIRECT],
+                                     P.d_scales_u8[SEC_DIRECT], P.d_dq_scale[SEC_DIRECT], P.d_codes[SEC_DIRECT],
+                                     P.d_topk_idx[1], P.d_topk_val[1], ke, err_gate, P.d_topk_idx[0],
+                                     P.d_topk_val[0], ko, d_dst, st);
+            return;
         } else {
             launch_quant_decode(N, H.quantization_only_format, P.d_scales_f32[SEC_DIRECT], P.d_scales_u8[SEC_DIRECT],
                                 P.d_dq_scale[SEC_DIRECT], P.d_codes[SEC_DIRECT], d_dst, st);

@@ -211,3 +211,32 @@ def test_device_resident_matches_abi(fmt, ro, re):
     assert np.array_equal(dst.download(np.float32, rows * cols).reshape(rows, cols), out)
     B.compress_release()
     B.decompress_release()
+
+
+@pytest.mark.parametrize("rows,cols,fmt,ro,re", [
+    (37, 101, B.NF4, 0.03, 0.07),        # ragged width: element-wise decode of the fused row pass
+    (33, 99, B.NF4_DQ, 0.02, 0.5),
+    (16, 2000, B.NF4, 0.2, 0.25),        # k = 400 and 500 per row: entries past the first 256
+    (8, 4096, B.NF4, 0.0, 0.3),          # error set only
+    (24, 4096, B.NF4_DQ, 0.05, 0.0),     # outlier set only
+    (64, 11008, B.NF4_DQ, 0.005, 0.01),  # the headline width
+])
+def test_device_resident_direct_decode_fused_with_the_scatter(rows, cols, fmt, ro, re):
+    """bsq_device_decompress decodes a direct section and adds both top-k sets
+    in one pass over the rows (error set gated by the compress flags, then the
+    outlier set); the result equals the host ABI's decode + scatter and the
+    oracle's decode bit for bit."""
+    x = ref_source(rows, cols, 0.13, 0.05)
+    x[::5, ::7] *= 40.0  # outlier columns in some rows
+    data, out, _ = run_direct(x, ro, re, fmt)
+    _, exp_out = oracle_direct(x, ro, re, fmt)
+    assert out.tobytes() == exp_out.tobytes()
+    src = B.DeviceBuffer.from_array(x)
+    dst = B.DeviceBuffer(rows * cols * 4)
+    dst.zero()
+    packed = B.device_compress(src)
+    B.device_decompress(packed, dst, rows * cols)
+    B.device_synchronize()
+    assert dst.download(np.float32, rows * cols).reshape(rows, cols).tobytes() == exp_out.tobytes()
+    B.compress_release()
+    B.decompress_release()
