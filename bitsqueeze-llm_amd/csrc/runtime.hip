@@ -19,11 +19,15 @@
 #include "bsq_internal.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <memory>
+#include <mutex>
+#include <thread>
 #include <vector>
 
 namespace bsq {
@@ -48,6 +52,103 @@ int cu_count() {
 namespace {
 
 thread_local std::string g_last_error;
+
+// Host copies of the packed payload (pinned staging <-> the caller's block)
+// split over a few persistent threads: one thread copies about 10-20 GB/s,
+// and a fresh calloc block also takes a page fault per 4 KB on first touch,
+// which threads take in parallel.  The caller's thread copies too; chunks of
+// 1 MB are taken from the job's atomic counter.  Each job is its own object,
+// held by every thread that works on it, so a late worker never touches the
+// next job's counters.  Calls are serialised.
+class CopyPool {
+  public:
+    static CopyPool &get() {
+        static CopyPool pool;
+        return pool;
+    }
+    void copy(void *dst, const void *src, size_t n) {
+        if (n < 2 * kChunk || workers_.empty()) {
+            if (src) std::memcpy(dst, src, n);
+            else std::memset(dst, 0, n);
+            return;
+        }
+        std::lock_guard<std::mutex> call(call_mu_);
+        auto job = std::make_shared<Job>();
+        job->dst = static_cast<uint8_t *>(dst);
+        job->src = static_cast<const uint8_t *>(src);
+        job->n = n;
+        job->chunks = (n + kChunk - 1) / kChunk;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            job_ = job;
+            ++seq_;
+        }
+        cv_.notify_all();
+        work(*job);
+        std::unique_lock<std::mutex> lk(job->mu);
+        job->cv.wait(lk, [&] { return job->done.load() == job->chunks; });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto &t : workers_) t.join();
+    }
+
+  private:
+    static constexpr size_t kChunk = 1u << 20;
+    struct Job {
+        uint8_t *dst = nullptr;
+        const uint8_t *src = nullptr;
+        size_t n = 0, chunks = 0;
+        std::atomic<size_t> next{0}, done{0};
+        std::mutex mu;
+        std::condition_variable cv;
+    };
+    CopyPool() {
+        const unsigned hw = std::thread::hardware_concurrency();
+        const unsigned n = std::min(7u, hw > 1 ? hw - 1 : 0u);
+        for (unsigned i = 0; i < n; ++i) workers_.emplace_back([this] { loop(); });
+    }
+    static void work(Job &j) {
+        size_t c;
+        while ((c = j.next.fetch_add(1)) < j.chunks) {
+            const size_t off = c * kChunk, len = std::min(kChunk, j.n - off);
+            if (j.src) std::memcpy(j.dst + off, j.src + off, len);
+            else std::memset(j.dst + off, 0, len);
+            if (j.done.fetch_add(1) + 1 == j.chunks) {
+                std::lock_guard<std::mutex> lk(j.mu);
+                j.cv.notify_all();
+            }
+        }
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            std::shared_ptr<Job> job;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || seq_ != seen; });
+                if (stop_) return;
+                seen = seq_;
+                job = job_;
+            }
+            work(*job);
+        }
+    }
+    std::vector<std::thread> workers_;
+    std::mutex mu_, call_mu_;
+    std::condition_variable cv_;
+    std::shared_ptr<Job> job_;
+    uint64_t seq_ = 0;
+    bool stop_ = false;
+};
+
+void host_copy(void *dst, const void *src, size_t n) { CopyPool::get().copy(dst, src, n); }
+// zeroes (and so faults in) a fresh host block with the same threads
+void host_touch(void *dst, size_t n) { CopyPool::get().copy(dst, nullptr, n); }
 
 void set_error(const char *msg) { g_last_error = msg ? msg : ""; }
 
@@ -763,12 +864,16 @@ bitsqz_llm_array_t *assemble_host(Runtime &rt, const bsq_device_packed_t &P) {
     std::unique_ptr<void, void (*)(void *)> block(std::calloc(1, 200 + full), std::free);
     BSQ_REQUIRE(block != nullptr, "calloc of the packed object failed");
     uint8_t *pl = static_cast<uint8_t *>(block.get()) + 200;
+    // calloc maps a large block lazily: its pages are faulted in by several
+    // threads while the copies above are still in flight, so the copies
+    // below run without faults
+    host_touch(pl, full);
     auto put_topk = [&](int t) {
         const bitsqz_section_t &d = *descs[4 + t];
         if (d.storage == BITSQZ_SECTION_NONE) return;
         const TopkHeader th{H.num_rows, H.num_columns, P.topk_k[t], 0};
         std::memcpy(pl + d.offset, &th, sizeof(th));
-        std::memcpy(pl + d.offset + 8, stage + d.offset + 8, d.size - 8);
+        host_copy(pl + d.offset + 8, stage + d.offset + 8, d.size - 8);
     };
     BSQ_HIP(hipEventSynchronize(rt.cev[0]));
     put_topk(0);
@@ -788,14 +893,11 @@ bitsqz_llm_array_t *assemble_host(Runtime &rt, const bsq_device_packed_t &P) {
             qh.block_size = kQuantBlock;
             qh.dq_scale = method == kMethodNF4DQ ? msec.dq[i] : 0.0f;
             std::memcpy(pl + d.offset, &qh, sizeof(qh));
-            std::memcpy(pl + d.offset + 48, stage + d.offset + 48, d.size - 48);
+            host_copy(pl + d.offset + 48, stage + d.offset + 48, d.size - 48);
         } else {
-            std::memcpy(pl + d.offset, stage + d.offset, d.size);
+            host_copy(pl + d.offset, stage + d.offset, d.size);
         }
     }
-    // first touch of the error blob's pages (calloc maps them lazily) while
-    // the device still computes it, so the page faults stay off the tail
-    if (descs[5]->storage != BITSQZ_SECTION_NONE) std::memset(pl + descs[5]->offset, 0, descs[5]->size);
     BSQ_HIP(hipEventSynchronize(rt.cev[2]));
     const Meta mend = *meta_end;
     const bool err_present = P.topk_k[1] > 0 && (mend.flags & kFlagError);
@@ -936,8 +1038,24 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
     const uint64_t stage_cap = rt.h_stage ? rt.h_stage_bytes - 2 * sizeof(Meta) : 0;
     auto staged = [&](const bitsqz_section_t &s) -> const uint8_t * {
         if (s.offset + s.size > stage_cap) return src;
-        std::memcpy(rt.h_stage + s.offset, src + s.offset, s.size);
+        host_copy(rt.h_stage + s.offset, src + s.offset, s.size);
         return rt.h_stage;
+    };
+    // payload bytes [off, off + n) to the device through the staging in
+    // pieces of 4 MB: each piece's H2D is issued as soon as the host has
+    // staged it, so the link works while the host stages the next
+    auto h2d_pieces = [&](void *dev, uint64_t off, uint64_t n, hipStream_t s) {
+        if (off + n > stage_cap) {
+            BSQ_HIP(hipMemcpyAsync(dev, src + off, n, hipMemcpyHostToDevice, s));
+            return;
+        }
+        constexpr uint64_t kPiece = 4ull << 20;
+        for (uint64_t q = 0; q < n; q += kPiece) {
+            const uint64_t len = std::min(kPiece, n - q);
+            host_copy(rt.h_stage + off + q, src + off + q, len);
+            BSQ_HIP(hipMemcpyAsync(static_cast<uint8_t *>(dev) + q, rt.h_stage + off + q, len,
+                                   hipMemcpyHostToDevice, s));
+        }
     };
     bsq_device_packed_t P{};
     P.header = *c;
@@ -984,8 +1102,7 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
     auto stage_section = [&](int i, const bitsqz_section_t &s, int method, uint64_t count, float *dense_dst) {
         if (s.storage == BITSQZ_SECTION_FP32) {
             BSQ_REQUIRE(s.size == count * 4, "FP32 section size mismatch");
-            const uint8_t *pl = staged(s);
-            BSQ_HIP(hipMemcpyAsync(dense_dst, pl + s.offset, count * 4, hipMemcpyHostToDevice, st));
+            h2d_pieces(dense_dst, s.offset, count * 4, st);
             P.d_dense[i] = dense_dst;
             P.count[i] = count;
             return;
@@ -994,9 +1111,11 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         BSQ_REQUIRE(rt.quant_initialized, "quantisation runtime missing");
         QuantHeader h;
         BSQ_REQUIRE(quant_blob_ok(src + s.offset, s.size, method, count, &h), "invalid quantised section");
-        const uint8_t *pl = staged(s);
         const uint64_t nb = h.num_blocks;
         const uint64_t ssz = method == kMethodNF4 ? nb * 4 : nb;
+        // the header and block scales staged at once, the codes piecewise
+        const bitsqz_section_t head{s.offset, 48 + ssz, s.storage};
+        const uint8_t *pl = staged(head);
         // packed U at the start of the staging, packed V after it
         const bool packed = keep_packed && (i == SEC_U || i == SEC_V);
         const uint64_t coff = !keep_packed ? 0 : (i == SEC_V ? v_code_off : (i == SEC_S ? s_code_off : 0));
@@ -1005,7 +1124,7 @@ void decompress_host(Runtime &rt, const bitsqz_llm_array_t *c, float *d_dst) {
         uint8_t *sc_u8 = rt.q_scales_u8 + soff, *codes = rt.q_codes + coff;
         void *sdst = method == kMethodNF4 ? static_cast<void *>(sc_f32) : static_cast<void *>(sc_u8);
         BSQ_HIP(hipMemcpyAsync(sdst, pl + s.offset + 48, ssz, hipMemcpyHostToDevice, st));
-        BSQ_HIP(hipMemcpyAsync(codes, pl + s.offset + 48 + ssz, (count + 1) / 2, hipMemcpyHostToDevice, st));
+        h2d_pieces(codes, s.offset + 48 + ssz, (count + 1) / 2, st);
         if (method == kMethodNF4DQ)
             BSQ_HIP(hipMemcpyAsync(&rt.meta->dq[i], pl + s.offset + 40, 4, hipMemcpyHostToDevice, st));
         P.count[i] = count;
