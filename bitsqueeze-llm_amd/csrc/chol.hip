@@ -1,10 +1,11 @@
 // Blocked Cholesky factorisation and triangular inverse for CholeskyQR
 // (k x k FP64 Gram matrices, k <= 256).
 //
-//   chol_blocked_kernel   one workgroup of 1024 lanes.  Waves 1..15 hold the
-//                         lower 16 x 16 tiles of the padded KP x KP matrix
-//                         (KP = 32 * NB) in MFMA accumulator layout; wave 0
-//                         factors and inverts the 32 x 32 diagonal blocks.
+//   chol_blocked_kernel   one workgroup of 1024 lanes.  The 12 waves that do
+//                         not share wave 0's SIMD hold the lower 16 x 16
+//                         tiles of the padded KP x KP matrix (KP = 32 * NB)
+//                         in MFMA accumulator layout; wave 0 factors and
+//                         inverts the 32 x 32 diagonal blocks.
 //                         Right-looking by 32-column panels with look-ahead:
 //                         the panel solve L_ij = A_ij L_jj^{-T} and the rank-32
 //                         trailing update run on the FP64 matrix cores, and
@@ -70,17 +71,6 @@ __device__ __forceinline__ double lane_fetch(double v, int src) {
 // Orders one wave's LDS accesses: wait for its outstanding LDS operations and
 // keep the compiler from moving memory accesses across.
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-__device__ double wg_max(double v, double *red) {
-    for (int off = 32; off >= 1; off >>= 1) v = fmax(v, __shfl_xor(v, off));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    double s = red[0];
-    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) s = fmax(s, red[w]);
-    return s;
-}
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
@@ -156,7 +146,7 @@ __device__ __forceinline__ bool gj_factor16(const double (*S)[PITCH], double (*L
 }
 
 // Factors the 32 x 32 diagonal block in Dg (lower triangle used) on one wave
-// and writes its inverse to LI (zeros above the diagonal) and to LIblk, by
+// and writes its inverse to LI (zeros above the diagonal), by
 // 2 x 2 blocks of 16:
 //   L11, L11^{-1} = gj_factor16(A11);   L21 = A21 L11^{-T};
 //   L22, L22^{-1} = gj_factor16(A22 - L21 L21^T);
@@ -168,8 +158,7 @@ __device__ __forceinline__ bool gj_factor16(const double (*S)[PITCH], double (*L
 // accumulator register u of lane l holds D[4 u + l / 16][l % 16].
 // Returns true when a pivot is <= tiny (or NaN).
 template <int PITCH>
-__device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*LI)[PITCH],
-                                                  double *__restrict__ LIblk, double tiny, int lane) {
+__device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*LI)[PITCH], double tiny, int lane) {
     const int kq = lane >> 4, cc = lane & 15;
     bool bad = gj_factor16<PITCH>(Dg, LI, tiny, lane);
 #pragma unroll
@@ -210,14 +199,28 @@ __device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*
         t = __builtin_amdgcn_mfma_f64_16x16x4f64(-LI[16 + cc][16 + 4 * s + kq], Dg[4 * s + kq][cc], t, 0, 0, 0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) LI[16 + 4 * u + kq][cc] = t[u];
-    wave_lds_fence();
-    // LI -> LIblk (32 x 32 row-major): 16 doubles per lane
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const int e = 64 * u + lane, r = e >> 5, c = e & 31;
-        LIblk[e] = LI[r][c];
-    }
     return bad;
+}
+
+// Tile (I, J) of G in the MFMA accumulator layout (register u of lane l holds
+// element (16 I + 4 u + l / 16, 16 J + l % 16)): G plus `shift` on the
+// diagonal inside, the identity in the padding; the loads are clamped into G
+// and masked, so no lane branches.  dm takes the max |G_ii| of the tile.
+__device__ __forceinline__ f64x4 load_tile(const double *__restrict__ G, int k, int I, int J, double shift, int kq,
+                                           int cc, double &dm) {
+    f64x4 t;
+    const int c = 16 * J + cc;
+    const unsigned cin = static_cast<unsigned>(c - k) >> 31;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = 16 * I + 4 * u + kq;
+        const unsigned inside = (static_cast<unsigned>(i - k) >> 31) & cin;
+        const unsigned diag = 1u - min(1u, static_cast<unsigned>(i ^ c));
+        const double g = G[static_cast<unsigned>(min(i, k - 1) * k + min(c, k - 1))];
+        t[u] = keep_if(g, inside) + static_cast<double>(diag) * (inside ? shift : 1.0);
+        dm = fmax(dm, keep_if(fabs(g), inside & diag));
+    }
+    return t;
 }
 
 // Lout: KP x KP row-major, the blocks below the diagonal blocks written (the
@@ -226,21 +229,27 @@ __device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*
 // status[0]: number of shifted restarts (7 = gave up, L = I).
 //
 // Right-looking by 32-column panels with look-ahead.  Wave 0 only factors the
-// diagonal blocks (factor_diag_block).  Waves 1..15 hold the lower 16 x 16
-// tiles (I >= J) of the padded matrix in the accumulator layout of
-// v_mfma_f64_16x16x4f64 (register u of lane l holds tile element
-// (4u + l / 16, l % 16)), ordered by column then row, wave w owning tiles
-// w - 1, w + 14, w + 29, ...; every trailing matrix is a suffix of that order,
-// so each step's tiles are spread over the 15 waves to within one.  Step jb:
-//   B1  wave 0 has factored block jb (LI);
-//       panel L_I,jb = A_I,jb L_jj^{-T} on the matrix cores (A from the LDS
-//       panel X, result to the LDS panel Y and to Lout);
+// diagonal blocks (factor_diag_block).  The lower 16 x 16 tiles (I >= J) of
+// the padded matrix in block columns 0 and 1 go straight from G to LDS
+// (block 0 -> Dg, panel 0 -> X); the other tiles are held in the accumulator
+// layout of v_mfma_f64_16x16x4f64 (register u of lane l holds tile element
+// (4u + l / 16, l % 16)) by the 12 waves that do not share wave 0's SIMD (a
+// workgroup's waves are dealt to the four SIMDs in turn, so waves 4, 8, 12
+// run beside wave 0: left without tiles, they keep the matrix core free for
+// the factorisation), ordered by column then row, so every trailing matrix
+// is a suffix of that order and each step's tiles are spread over the 12
+// waves to within one.  Step jb:
+//   B1  wave 0 has factored block jb (LI); waves 1..15 copy LI to LIout and
+//       form the panel L_I,jb = A_I,jb L_jj^{-T} on the matrix cores (A from
+//       the LDS panel X, result to the LDS panel Y and to Lout), its tiles
+//       dealt over all 15 waves;
 //   B2  the diagonal block jb + 1 takes its update A -= L L^T first and goes
 //       to Dg;
-//   B3  wave 0 factors block jb + 1 while waves 1..15 update the rest of the
-//       trailing matrix and copy the next panel into X.
+//   B3  wave 0 factors block jb + 1 while the tile holders update the rest of
+//       the trailing matrix and copy the next panel into X.
 // The products read their operands from LDS: two 8-byte reads per
-// 16 x 16 x 4 product.
+// 16 x 16 x 4 product.  The breakdown threshold is relative to max |G_ii|,
+// taken from the diagonal tiles as they load.
 template <int NB>
 __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double *__restrict__ G, int k,
                                                                      double *__restrict__ Lout,
@@ -249,8 +258,13 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
                                                                      const int *__restrict__ run) {
     if (run && run[0] == 0) return;  // uniform: the refinement step replaced this pass
     constexpr int KP = NB * 32, NT = 2 * NB, NTILES = NT * (NT + 1) / 2;
-    constexpr int TW = kCholThreads / 64 - 1, SLOTS = (NTILES + TW - 1) / TW;
+    constexpr int C01 = 2 * NT - 1;  // tiles in block columns 0 and 1
+    constexpr int OW = 12;           // tile-holding waves
+    constexpr int HS = (NTILES - C01 + OW - 1) / OW, LS = (C01 + 3) / 4;  // held, loaded-only tiles per wave
+    constexpr int SLOTS = HS > LS ? HS : LS;
+    constexpr int PSLOTS = (2 * (NT - 2) + 14) / 15 > 0 ? (2 * (NT - 2) + 14) / 15 : 1;  // panel tiles per wave
     constexpr int PR = (NB > 1) ? (NB - 1) * 32 : 1;
+    static_assert(kCholThreads == 1024, "16 waves: wave 0 and three tile-free waves on one SIMD");
     // pitch 33 (odd): the MFMA operand reads (16 rows, one column each) and the
     // tile stores (one row, 16 columns) hit 32 distinct banks per 16 lanes
     constexpr int PITCH = 33;
@@ -261,26 +275,64 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
     __shared__ double red[kCholThreads / 64];
     __shared__ int broke;
 
-    double dmax = 0.0;
-    for (int i = threadIdx.x; i < k; i += kCholThreads) dmax = fmax(dmax, fabs(G[static_cast<uint64_t>(i) * k + i]));
-    dmax = wg_max(dmax, red);
-    const double tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    double shift = 0.0;
+    double shift = 0.0, dmax = 0.0, tiny = 0.0;
     int attempt = 0;
     bool identity = false;
     for (;; ++attempt) {
         if (threadIdx.x == 0) broke = 0;
         bool failed = false;
+        // slots: waves w % 4 != 0 hold tiles C01 + OW m + (w - 1 - w / 4) for the
+        // whole factorisation; waves 0, 4, 8, 12 load the tiles 4 m + w / 4 of
+        // block columns 0, 1 into LDS
+        int tI[SLOTS], tJ[SLOTS];
+#pragma unroll
+        for (int m = 0; m < SLOTS; ++m) {
+            const int idx = ((wave & 3) == 0) ? (4 * m + (wave >> 2) < C01 ? 4 * m + (wave >> 2) : NTILES)
+                                              : C01 + OW * m + wave - 1 - (wave >> 2);
+            tile_coords<NT>(idx < NTILES ? idx : 0, tI[m], tJ[m]);
+            if (idx >= NTILES) tJ[m] = -1;  // no tile in this slot
+        }
+        f64x4 acc[SLOTS];
+        {
+            const int lane = opaque(static_cast<int>(threadIdx.x)) & 63, kq = lane >> 4, cc = lane & 15;
+            double dm = 0.0;
+#pragma unroll
+            for (int m = 0; m < SLOTS; ++m)
+                acc[m] = (tJ[m] < 0) ? f64x4{0.0, 0.0, 0.0, 0.0}  // uniform
+                                     : load_tile(G, k, tI[m], tJ[m], shift, kq, cc, dm);
+#pragma unroll
+            for (int m = 0; m < SLOTS; ++m) {
+                const int I = tI[m], J = tJ[m];
+                if (J == 0 || J == 1) {  // uniform
+                    if (I < 2) {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) Dg[16 * I + 4 * u + kq][16 * J + cc] = acc[m][u];
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) X[16 * (I - 2) + 4 * u + kq][16 * J + cc] = acc[m][u];
+                    }
+                }
+            }
+            if (attempt == 0) {
+                for (int off = 32; off >= 1; off >>= 1) dm = fmax(dm, __shfl_xor(dm, off));
+                if (lane == 0) red[wave] = dm;
+            }
+        }
+        __syncthreads();  // P0: block 0 is in Dg, panel 0 in X, the diagonal maxima in red
+        if (attempt == 0) {
+#pragma unroll
+            for (int w = 0; w < kCholThreads / 64; ++w) dmax = fmax(dmax, red[w]);
+            tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
+        }
         if (wave == 0) {
             // the factorisation wave (issued first on its SIMD: it is the
-            // critical path); the same barrier sequence as the tile waves
+            // critical path); the same barrier sequence as the other waves
             __builtin_amdgcn_s_setprio(3);
-            __syncthreads();  // P0: block 0 is in Dg
 #pragma unroll 1
             for (int jb = 0; jb < NB; ++jb) {
                 const int lane = opaque(static_cast<int>(threadIdx.x)) & 63;
-                const bool bad = factor_diag_block<PITCH>(Dg, LI, LIout + static_cast<uint64_t>(jb) * 1024, tiny, lane);
+                const bool bad = factor_diag_block<PITCH>(Dg, LI, tiny, lane);
                 if (bad && lane == 0) broke = 1;
                 __syncthreads();  // B1
                 if (broke) {
@@ -294,53 +346,6 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
             }
             __builtin_amdgcn_s_setprio(0);
         } else {
-            int tI[SLOTS], tJ[SLOTS];
-#pragma unroll
-            for (int m = 0; m < SLOTS; ++m) {
-                const int idx = TW * m + wave - 1;
-                tile_coords<NT>(idx < NTILES ? idx : 0, tI[m], tJ[m]);
-                if (idx >= NTILES) tJ[m] = -1;  // no tile in this slot
-            }
-            f64x4 acc[SLOTS];
-            {
-                const int lane = opaque(static_cast<int>(threadIdx.x)) & 63, kq = lane >> 4, cc = lane & 15;
-#pragma unroll
-                for (int m = 0; m < SLOTS; ++m) {
-                    if (tJ[m] < 0) {  // uniform
-                        acc[m] = f64x4{0.0, 0.0, 0.0, 0.0};
-                        continue;
-                    }
-                    // G (+ shift on the diagonal) inside, identity in the padding; the
-                    // loads are clamped into G and masked, so no lane branches
-                    const int c = 16 * tJ[m] + cc;
-                    const unsigned cin = static_cast<unsigned>(c - k) >> 31;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const int i = 16 * tI[m] + 4 * u + kq;
-                        const unsigned inside = (static_cast<unsigned>(i - k) >> 31) & cin;
-                        const unsigned diag = 1u - min(1u, static_cast<unsigned>(i ^ c));
-                        const double g = G[static_cast<unsigned>(min(i, k - 1) * k + min(c, k - 1))];
-                        acc[m][u] = keep_if(g, inside) + static_cast<double>(diag) * (inside ? shift : 1.0);
-                    }
-                }
-                // block 0 -> Dg (lower tiles), panel 0 -> X
-#pragma unroll
-                for (int m = 0; m < SLOTS; ++m) {
-                    const int I = tI[m], J = tJ[m];
-                    if (J == 0 || J == 1) {
-                        if (I < 2) {
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) {
-                                Dg[16 * I + 4 * u + kq][16 * J + cc] = acc[m][u];
-                            }
-                        } else {
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) X[16 * (I - 2) + 4 * u + kq][16 * J + cc] = acc[m][u];
-                        }
-                    }
-                }
-            }
-            __syncthreads();  // P0
             // jb stays a loop: the tile registers are indexed by slot only
 #pragma unroll 1
             for (int jb = 0; jb < NB; ++jb) {
@@ -350,18 +355,27 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
                     failed = true;
                     break;
                 }
+                {
+                    // LI -> LIout block jb (32 x 32 row-major): 960 lanes, e and e + 960
+                    double *LIblk = LIout + static_cast<uint64_t>(jb) * 1024;
+                    const int e = 64 * (wave - 1) + lane;
+                    LIblk[e] = LI[e >> 5][e & 31];
+                    if (e < 1024 - 960) LIblk[e + 960] = LI[(e + 960) >> 5][e & 31];
+                }
                 if (jb + 1 < NB) {
-                    // panel: A[r][q] = X[row r][4s + q], B[q][c] = LI[c][4s + q]
-                    // (LI is lower triangular: its first 16 rows end at column 15)
+                    // panel tiles q = 15 m + wave - 1: column 2 jb + (q & 1), row
+                    // 2 jb + 2 + (q >> 1); A[r][q] = X[row r][4s + q], B[q][c] =
+                    // LI[c][4s + q] (LI is lower triangular: its first 16 rows end
+                    // at column 15)
 #pragma unroll
-                    for (int m = 0; m < SLOTS; ++m) {
-                        const int I = tI[m], J = tJ[m];
-                        if ((J == 2 * jb || J == 2 * jb + 1) && I >= 2 * jb + 2) {
+                    for (int m = 0; m < PSLOTS; ++m) {
+                        const int q = 15 * m + wave - 1, J = 2 * jb + (q & 1), I = 2 * jb + 2 + (q >> 1);
+                        if (q < 2 * (NT - 2 * jb - 2)) {  // uniform
                             const int pr = 16 * (I - 2 * jb - 2), lc16 = 16 * (J - 2 * jb);
                             f64x4 t = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
                             for (int s = 0; s < 8; ++s)
-                                if (s < 4 || J == 2 * jb + 1)
+                                if (s < 4 || (q & 1))
                                     t = __builtin_amdgcn_mfma_f64_16x16x4f64(X[pr + cc][4 * s + kq],
                                                                              LI[lc16 + cc][4 * s + kq], t, 0, 0, 0);
 #pragma unroll
@@ -386,9 +400,7 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
                                 t = __builtin_amdgcn_mfma_f64_16x16x4f64(-Y[pa + cc][4 * s + kq], Y[pb + cc][4 * s + kq],
                                                                          t, 0, 0, 0);
 #pragma unroll
-                            for (int u = 0; u < 4; ++u) {
-                                Dg[pa + 4 * u + kq][pb + cc] = t[u];
-                            }
+                            for (int u = 0; u < 4; ++u) Dg[pa + 4 * u + kq][pb + cc] = t[u];
                         }
                     }
                     __syncthreads();  // B3: wave 0 factors block jb + 1 meanwhile
