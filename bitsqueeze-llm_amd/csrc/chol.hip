@@ -85,15 +85,39 @@ __device__ __forceinline__ void tile_coords(int idx, int &I, int &J) {
     I = j + idx - (j * NT - j * (j - 1) / 2);
 }
 
-// Cholesky factor and inverse of the 16 x 16 block S[0..16)[0..16) (lower
+// 1 / d for a positive normal d: the hardware reciprocal estimate refined by
+// two Newton steps, each of which doubles the number of correct bits.
+__device__ __forceinline__ double recip_nr(double d) {
+    double r = __builtin_amdgcn_rcp(d);
+    r = fma(r, fma(-d, r, 1.0), r);
+    return fma(r, fma(-d, r, 1.0), r);
+}
+
+// value of `v` in lane l - 1 (within each row of 16 lanes)
+__device__ __forceinline__ double lane_below(double v) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_mov_dpp(static_cast<int>(u & 0xffffffffu), 0x111, 0xF, 0xF, true));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_mov_dpp(static_cast<int>(u >> 32), 0x111, 0xF, 0xF, true));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// Inverse Cholesky factor of the 16 x 16 block S[0..16)[0..16) (lower
 // triangle used) on one wave: 8 x 8 lane grid, lane (lr, lc) holding the 2 x 2
-// sub-blocks a = A[2lr.., 2lc..] and x = X[2lr.., 2lc..] of the block and of
-// its inverse (X starts as I).  Step t: scale column t of A and row t of X by
-// 1/sqrt(pivot), fetch the two column-t values of this lane's rows and
-// columns and the two row-t values of X with lane permutes, then rank-1
-// update A's trailing columns and X's trailing rows (Gauss-Jordan on [L | I]
-// fused into the factorisation).  Writes L^{-1} (zeros above the diagonal) to
-// LIo; returns true when a pivot is <= tiny (or NaN).
+// sub-blocks a[p][q] = A[2lr + p][2lc + q] of the block and x[p][q] =
+// X[2lc + p][2lr + q] of the unscaled inverse (X starts as I; held transposed,
+// so that row t + 1 of X sits in the lanes of column t + 1 of A).  Step t
+// (pivot d = A[t][t]) is the rank-1 update A[i][c] -= A[i][t] A[c][t] / d for
+// columns c > t and X[i] -= (A[i][t] / d) X[t] for rows i > t (Gauss-Jordan on
+// [L | I] fused into the factorisation, the square roots deferred: with
+// L[i][t] = A[i][t] / sqrt(d), row t of L^{-1} is X[t] / sqrt(d)).  It runs
+// with look-ahead: column t + 1 of A and row t + 1 of X go first (their
+// column-t inputs are in the same lane or one lane down, and A[t + 1][t] is one
+// scalar read), so the next pivot and its reciprocal follow at once; the
+// update of the columns and rows beyond t + 1 reads its inputs through lane
+// permutes issued one step ahead.  Only the inverse is needed, so L itself is
+// never formed: the pivots stay on A's diagonal and scale X's rows at the end.
+// Writes L^{-1} (zeros above the diagonal) to LIo; returns true when a pivot
+// is <= tiny (or NaN).
 template <int PITCH>
 __device__ __forceinline__ bool gj_factor16(const double (*S)[PITCH], double (*LIo)[PITCH], double tiny, int lane) {
     const int lr = lane >> 3, lc = lane & 7;
@@ -106,42 +130,73 @@ __device__ __forceinline__ bool gj_factor16(const double (*S)[PITCH], double (*L
             a[p][q] = S[2 * lr + p][2 * lc + q];
             x[p][q] = (p == q) ? on_diag : 0.0;
         }
-    bool bad = false;
+    const double d0 = lane_value(a[0][0], 0);
+    bool bad = !(d0 > tiny);
+    double rd = recip_nr(d0);
+    // step-t inputs of the trailing update: A[2lr + p][t], A[2lc + p][t], X[t][2lr + q]
+    double lrow[2], lcol[2], xrow[2];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        const int tb = t >> 1, tq = t & 1;
-        const double dtt = lane_value(a[tq][tq], tb * 9);
-        bad = bad || !(dtt > tiny);
-        const double inv = rsqrt(dtt);
-        const double fc = (lc == tb) ? inv : 1.0, fr = (lr == tb) ? inv : 1.0;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) a[p][tq] *= fc;  // column t of L (row t: sqrt(pivot))
-#pragma unroll
-        for (int q = 0; q < 2; ++q) x[tq][q] *= fr;  // row t of L^{-1}
-        double lrow[2], lcol[2], xrow[2];
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            lrow[p] = lane_fetch(a[p][tq], lr * 8 + tb);  // L[2lr + p][t]
-            lcol[p] = lane_fetch(a[p][tq], lc * 8 + tb);  // L[2lc + p][t]
-            xrow[p] = lane_fetch(x[tq][p], tb * 8 + lc);  // X[t][2lc + p]
-        }
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            // only columns c > t of A and rows i > t of X change; the lower
-            // triangle of A is all that feeds L
-            const double cb = keep_if(lcol[p], static_cast<unsigned>(t - (2 * lc + p)) >> 31);
-            const double rb = keep_if(lrow[p], static_cast<unsigned>(t - (2 * lr + p)) >> 31);
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                a[q][p] = fma(-lrow[q], cb, a[q][p]);
-                x[p][q] = fma(-rb, xrow[q], x[p][q]);
-            }
-        }
+    for (int p = 0; p < 2; ++p) {
+        lrow[p] = lane_fetch(a[p][0], lr * 8);
+        lcol[p] = lane_fetch(a[p][0], lc * 8);
+        xrow[p] = lane_fetch(x[0][p], lr * 8);
     }
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int t = 0; t < 15; ++t) {
+        const int tb = t >> 1, tq = t & 1, tb1 = (t + 1) >> 1, tq1 = (t + 1) & 1;
+        // column t + 1 of A and row t + 1 of X (lanes lc == tb1); their column-t
+        // and row-t inputs: this lane (t even) or the lane below (t odd)
+        const double at = lane_value(a[tq1][tq], tb1 * 8 + tb);  // A[t + 1][t]
+        const double sv = keep_if(at * rd, lc == tb1 ? 1u : 0u);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) LIo[2 * lr + p][2 * lc + q] = x[p][q];
+        for (int p = 0; p < 2; ++p) {
+            const double colt = tq ? lane_below(a[p][1]) : a[p][0];  // A[2lr + p][t]
+            a[p][tq1] = fma(-colt, sv, a[p][tq1]);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const double rowt = tq ? lane_below(x[1][q]) : x[0][q];  // X[t][2lr + q]
+            x[tq1][q] = fma(-sv, rowt, x[tq1][q]);
+        }
+        const double dn = lane_value(a[tq1][tq1], tb1 * 9);
+        bad = bad || !(dn > tiny);
+        const double rdn = recip_nr(dn);
+        double nrow[2], ncol[2], nxrow[2];
+        if (t + 2 < 16) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                nrow[p] = lane_fetch(a[p][tq1], lr * 8 + tb1);
+                ncol[p] = lane_fetch(a[p][tq1], lc * 8 + tb1);
+                nxrow[p] = lane_fetch(x[tq1][p], lr * 8 + tb1);
+            }
+            // columns c > t + 1 of A and rows i > t + 1 of X (the same index
+            // 2lc + p): column t + 1 keeps its pivot, and A's lower triangle is
+            // all that feeds X
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const double cb = keep_if(lcol[p] * rd, static_cast<unsigned>(t + 1 - (2 * lc + p)) >> 31);
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    a[q][p] = fma(-lrow[q], cb, a[q][p]);
+                    x[p][q] = fma(-cb, xrow[q], x[p][q]);
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                lrow[p] = nrow[p];
+                lcol[p] = ncol[p];
+                xrow[p] = nxrow[p];
+            }
+        }
+        rd = rdn;
+    }
+    // row i of L^{-1} = X[i] / sqrt(pivot i); pivot 2lc + p sits in lane (lc, lc)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const double inv = rsqrt(lane_fetch(a[p][p], lc * 9));
+#pragma unroll
+        for (int q = 0; q < 2; ++q) LIo[2 * lc + p][2 * lr + q] = x[p][q] * inv;
+    }
     return bad;
 }
 
