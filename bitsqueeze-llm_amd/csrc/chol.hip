@@ -259,11 +259,19 @@ __device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*
 
 // Tile (I, J) of G in the MFMA accumulator layout (register u of lane l holds
 // element (16 I + 4 u + l / 16, 16 J + l % 16)): G plus `shift` on the
-// diagonal inside, the identity in the padding; the loads are clamped into G
-// and masked, so no lane branches.  dm takes the max |G_ii| of the tile.
+// diagonal inside, the identity in the padding.  dm takes the max |G_ii| of
+// the tile.  Off-diagonal tiles inside G (the common case) are plain loads
+// from a wave-uniform base; the others clamp their loads into G and mask
+// them, so no lane branches.
 __device__ __forceinline__ f64x4 load_tile(const double *__restrict__ G, int k, int I, int J, double shift, int kq,
                                            int cc, double &dm) {
     f64x4 t;
+    if (I != J && 16 * I + 16 <= k && 16 * J + 16 <= k) {  // uniform
+        const double *__restrict__ g0 = G + static_cast<size_t>(16 * I) * k + 16 * J;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = g0[static_cast<size_t>(4 * u) * k + kq * k + cc];
+        return t;
+    }
     const int c = 16 * J + cc;
     const unsigned cin = static_cast<unsigned>(c - k) >> 31;
 #pragma unroll
