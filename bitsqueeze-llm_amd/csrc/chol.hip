@@ -72,6 +72,16 @@ __device__ __forceinline__ double lane_fetch(double v, int src) {
 // keep the compiler from moving memory accesses across.
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Workgroup barrier for data exchanged through LDS only: waits for this wave's
+// LDS operations but not for its global loads and stores, so loads into
+// registers stay in flight across it (their first use waits for them) and the
+// stores of L drain behind the next steps.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
 // Lower 16 x 16 tile number idx of an NT x NT tile grid, tiles ordered by
@@ -259,12 +269,11 @@ __device__ __forceinline__ bool factor_diag_block(double (*Dg)[PITCH], double (*
 
 // Tile (I, J) of G in the MFMA accumulator layout (register u of lane l holds
 // element (16 I + 4 u + l / 16, 16 J + l % 16)): G plus `shift` on the
-// diagonal inside, the identity in the padding.  dm takes the max |G_ii| of
-// the tile.  Off-diagonal tiles inside G (the common case) are plain loads
-// from a wave-uniform base; the others clamp their loads into G and mask
-// them, so no lane branches.
+// diagonal inside, the identity in the padding.  Off-diagonal tiles inside G
+// (the common case) are plain loads from a wave-uniform base; the others clamp
+// their loads into G and mask them, so no lane branches.
 __device__ __forceinline__ f64x4 load_tile(const double *__restrict__ G, int k, int I, int J, double shift, int kq,
-                                           int cc, double &dm) {
+                                           int cc) {
     f64x4 t;
     if (I != J && 16 * I + 16 <= k && 16 * J + 16 <= k) {  // uniform
         const double *__restrict__ g0 = G + static_cast<size_t>(16 * I) * k + 16 * J;
@@ -281,7 +290,6 @@ __device__ __forceinline__ f64x4 load_tile(const double *__restrict__ G, int k, 
         const unsigned diag = 1u - min(1u, static_cast<unsigned>(i ^ c));
         const double g = G[static_cast<unsigned>(min(i, k - 1) * k + min(c, k - 1))];
         t[u] = keep_if(g, inside) + static_cast<double>(diag) * (inside ? shift : 1.0);
-        dm = fmax(dm, keep_if(fabs(g), inside & diag));
     }
     return t;
 }
@@ -311,8 +319,8 @@ __device__ __forceinline__ f64x4 load_tile(const double *__restrict__ G, int k, 
 //   B3  wave 0 factors block jb + 1 while the tile holders update the rest of
 //       the trailing matrix and copy the next panel into X.
 // The products read their operands from LDS: two 8-byte reads per
-// 16 x 16 x 4 product.  The breakdown threshold is relative to max |G_ii|,
-// taken from the diagonal tiles as they load.
+// 16 x 16 x 4 product.  The barriers are on LDS only: the held tiles load
+// while block 0 is factored, and the stores of L drain behind the next steps.
 template <int NB>
 __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double *__restrict__ G, int k,
                                                                      double *__restrict__ Lout,
@@ -357,54 +365,68 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
             if (idx >= NTILES) tJ[m] = -1;  // no tile in this slot
         }
         f64x4 acc[SLOTS];
+        if (wave == 0) __builtin_amdgcn_s_setprio(3);  // its loads and the factorisation are the critical path
         {
             const int lane = opaque(static_cast<int>(threadIdx.x)) & 63, kq = lane >> 4, cc = lane & 15;
-            double dm = 0.0;
+            if (attempt == 0 && wave == 0) {
+                // breakdown scale max |G_ii|, for wave 0 (tiny) and, through
+                // LDS, the others (the shift of a restart)
+                double dm = 0.0;
+#pragma unroll
+                for (int m = 0; m < (KP + 63) / 64; ++m) {
+                    const int i = lane + 64 * m;
+                    const double g = G[static_cast<unsigned>(min(i, k - 1)) * static_cast<unsigned>(k + 1)];
+                    dm = fmax(dm, keep_if(fabs(g), static_cast<unsigned>(i - k) >> 31));
+                }
+                for (int off = 32; off >= 1; off >>= 1) dm = fmax(dm, __shfl_xor(dm, off));
+                dmax = dm;
+                tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
+                if (lane == 0) red[0] = dm;
+            }
+            // waves 0, 4, 8, 12 load first: their tiles (block columns 0, 1) go to
+            // LDS before P0; the other waves issue the loads of their held
+            // tiles after P0, so those do not delay block 0 and stay in flight
+            // across the LDS-only barriers while wave 0 factors block 0 (each
+            // wave passes one barrier here)
+            if ((wave & 3) != 0) lds_barrier();  // P0
 #pragma unroll
             for (int m = 0; m < SLOTS; ++m)
                 acc[m] = (tJ[m] < 0) ? f64x4{0.0, 0.0, 0.0, 0.0}  // uniform
-                                     : load_tile(G, k, tI[m], tJ[m], shift, kq, cc, dm);
+                                     : load_tile(G, k, tI[m], tJ[m], shift, kq, cc);
+            if ((wave & 3) == 0) {
 #pragma unroll
-            for (int m = 0; m < SLOTS; ++m) {
-                const int I = tI[m], J = tJ[m];
-                if (J == 0 || J == 1) {  // uniform
-                    if (I < 2) {
+                for (int m = 0; m < SLOTS; ++m) {
+                    const int I = tI[m], J = tJ[m];
+                    if (J >= 0) {  // uniform
+                        if (I < 2) {
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) Dg[16 * I + 4 * u + kq][16 * J + cc] = acc[m][u];
-                    } else {
+                            for (int u = 0; u < 4; ++u) Dg[16 * I + 4 * u + kq][16 * J + cc] = acc[m][u];
+                        } else {
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) X[16 * (I - 2) + 4 * u + kq][16 * J + cc] = acc[m][u];
+                            for (int u = 0; u < 4; ++u) X[16 * (I - 2) + 4 * u + kq][16 * J + cc] = acc[m][u];
+                        }
                     }
                 }
-            }
-            if (attempt == 0) {
-                for (int off = 32; off >= 1; off >>= 1) dm = fmax(dm, __shfl_xor(dm, off));
-                if (lane == 0) red[wave] = dm;
+                lds_barrier();  // P0: block 0 is in Dg, panel 0 in X, max |G_ii| in red[0]
             }
         }
-        __syncthreads();  // P0: block 0 is in Dg, panel 0 in X, the diagonal maxima in red
-        if (attempt == 0) {
-#pragma unroll
-            for (int w = 0; w < kCholThreads / 64; ++w) dmax = fmax(dmax, red[w]);
-            tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
-        }
+        if (attempt == 0) dmax = red[0];
         if (wave == 0) {
             // the factorisation wave (issued first on its SIMD: it is the
             // critical path); the same barrier sequence as the other waves
-            __builtin_amdgcn_s_setprio(3);
 #pragma unroll 1
             for (int jb = 0; jb < NB; ++jb) {
                 const int lane = opaque(static_cast<int>(threadIdx.x)) & 63;
                 const bool bad = factor_diag_block<PITCH>(Dg, LI, tiny, lane);
                 if (bad && lane == 0) broke = 1;
-                __syncthreads();  // B1
+                lds_barrier();  // B1
                 if (broke) {
                     failed = true;
                     break;
                 }
                 if (jb + 1 < NB) {
-                    __syncthreads();  // B2
-                    __syncthreads();  // B3
+                    lds_barrier();  // B2
+                    lds_barrier();  // B3
                 }
             }
             __builtin_amdgcn_s_setprio(0);
@@ -413,7 +435,7 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
 #pragma unroll 1
             for (int jb = 0; jb < NB; ++jb) {
                 const int lane = opaque(static_cast<int>(threadIdx.x)) & 63, kq = lane >> 4, cc = lane & 15;
-                __syncthreads();  // B1: LI holds block jb's inverse
+                lds_barrier();  // B1: LI holds block jb's inverse
                 if (broke) {
                     failed = true;
                     break;
@@ -448,7 +470,7 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
                             }
                         }
                     }
-                    __syncthreads();  // B2: Y holds the panel of L
+                    lds_barrier();  // B2: Y holds the panel of L
                     // trailing update A_IJ -= L_I,jb L_J,jb^T (2 jb + 2 <= J <= I):
                     // first the diagonal block jb + 1, which goes to Dg
                     const int nb0 = 2 * jb + 2;
@@ -466,7 +488,7 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
                             for (int u = 0; u < 4; ++u) Dg[pa + 4 * u + kq][pb + cc] = t[u];
                         }
                     }
-                    __syncthreads();  // B3: wave 0 factors block jb + 1 meanwhile
+                    lds_barrier();  // B3: wave 0 factors block jb + 1 meanwhile
 #pragma unroll
                     for (int m = 0; m < SLOTS; ++m) {
                         const int I = tI[m], J = tJ[m];

@@ -515,8 +515,14 @@ void decompress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int
 
 // The device-resident compress pipeline (src/bitsqz_llm.cu:981-1247 without
 // the host copies).  Everything is enqueued on rt.stream.
-void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
+void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, const bool stage_events) {
     const hipStream_t st = rt.stream;
+    // stage boundaries for the host path (its copy stream waits on them, and
+    // the profile reports their spans); each record costs the queue a few
+    // microseconds of idle time, so the device-resident path skips them
+    auto mark = [&](int i) {
+        if (stage_events) BSQ_HIP(hipEventRecord(rt.ev[i], st));
+    };
     const uint32_t rows = rt.rows, cols = rt.cols;
     const uint64_t N = static_cast<uint64_t>(rows) * cols;
     bsq_device_packed_t P{};
@@ -534,7 +540,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
     uint32_t flags = 0;
 
     BSQ_HIP(hipMemsetAsync(&rt.meta->flags, 0, sizeof(uint32_t), st));
-    BSQ_HIP(hipEventRecord(rt.ev[0], st));
+    mark(0);
 
     // outlier separation (topk_separation, src/bitsqz_llm.cu:1045-1056)
     const float *residual = d_in;
@@ -556,7 +562,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
         residual = rt.d_residual;
         flags |= kFlagOutlier;
     }
-    BSQ_HIP(hipEventRecord(rt.ev[1], st));
+    mark(1);
 
     TopkBuf &te = rt.topk[TK_ERROR];
     const bool has_svd = rt.svd_ranks >= 1;
@@ -565,7 +571,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
         H.effective_rank = static_cast<int16_t>(rt.q);
         Section &U = rt.sec[SEC_U], &S = rt.sec[SEC_S], &V = rt.sec[SEC_V];
         svd_run(rt.svd, residual, rt.sketch, 1241ULL, U.dense, S.dense, V.dense, st);
-        BSQ_HIP(hipEventRecord(rt.ev[2], st));
+        mark(2);
         // quantise U, S, V, each dequantised in place afterwards
         // (append_quantized_section with d_dequantized_dst = the source,
         // src/bitsqz_llm.cu:1078-1139)
@@ -575,20 +581,20 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
             launch_quant_encode(sc.dense, sc.count, sc.method, sc.scales_f32, sc.scales_u8, &rt.meta->dq[i],
                                 sc.codes, &rt.meta->gmax, st);
         }
-        BSQ_HIP(hipEventRecord(rt.ev[3], st));
+        mark(3);
         for (int i = 0; i < 3; ++i) {
             Section &sc = rt.sec[i];
             if (sc.method == kMethodNone) continue;
             launch_quant_decode(sc.count, sc.method, sc.scales_f32, sc.scales_u8, &rt.meta->dq[i], sc.codes,
                                 sc.dense, st);
         }
-        BSQ_HIP(hipEventRecord(rt.ev[4], st));
+        mark(4);
         if (te.capacity > 0) {
             // reconstruct + subtract fused (src/bitsqz_llm.cu:1141-1163)
             timed_gemm(kTimeReconstruct, st, [&] {
                 launch_reconstruct(U.dense, S.dense, V.dense, rows, cols, rt.q, residual, rt.d_err, st);
             });
-            BSQ_HIP(hipEventRecord(rt.ev[5], st));
+            mark(5);
             TopkArgs a;
             a.a = rt.d_err;
             a.rows = rows;
@@ -599,11 +605,11 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
             a.flags = &rt.meta->flags;
             launch_topk_select(a, st);
         } else {
-            BSQ_HIP(hipEventRecord(rt.ev[5], st));
+            mark(5);
         }
     } else {
         Section &D = rt.sec[SEC_DIRECT];
-        BSQ_HIP(hipEventRecord(rt.ev[2], st));
+        mark(2);
         if (D.method != kMethodNone) {
             D.dense = nullptr;
             if (have_row_gmax && D.method == kMethodNF4DQ)
@@ -612,9 +618,9 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
             else
                 launch_quant_encode(residual, N, D.method, D.scales_f32, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
                                     D.codes, &rt.meta->gmax, st);
-            BSQ_HIP(hipEventRecord(rt.ev[3], st));
-            BSQ_HIP(hipEventRecord(rt.ev[4], st));
-            BSQ_HIP(hipEventRecord(rt.ev[5], st));
+            mark(3);
+            mark(4);
+            mark(5);
             if (te.capacity > 0) {
                 // error = residual - dequant(direct), computed inside the top-k
                 // kernel (src/bitsqz_llm.cu:1183-1227)
@@ -643,12 +649,12 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out) {
             if (residual != rt.d_residual)
                 BSQ_HIP(hipMemcpyAsync(rt.d_residual, residual, N * 4, hipMemcpyDeviceToDevice, st));
             D.dense = rt.d_residual;
-            BSQ_HIP(hipEventRecord(rt.ev[3], st));
-            BSQ_HIP(hipEventRecord(rt.ev[4], st));
-            BSQ_HIP(hipEventRecord(rt.ev[5], st));
+            mark(3);
+            mark(4);
+            mark(5);
         }
     }
-    BSQ_HIP(hipEventRecord(rt.ev[6], st));
+    mark(6);
     BSQ_HIP(hipGetLastError());
 
     // descriptors: offsets are final except that the error section's
@@ -1273,7 +1279,7 @@ int bitsqz_llm_compress(const float *row_major_matrix_float_data, bitsqz_llm_arr
                 d_in = rt.d_stage;
             }
             bsq_device_packed_t P{};
-            compress_device(rt, d_in, &P);
+            compress_device(rt, d_in, &P, true);
             bitsqz_llm_array_t *buf = assemble_host(rt, P);
             BSQ_HIP(hipEventRecord(t_end, rt.stream));
             BSQ_HIP(hipEventSynchronize(t_end));
@@ -1429,7 +1435,7 @@ int bsq_device_compress(const float *d_input, bsq_device_packed_t *out) {
         set_error("bsq_device_compress: runtime not initialised or null argument");
         return 1;
     }
-    return guarded([&] { compress_device(g_comp, d_input, out); });
+    return guarded([&] { compress_device(g_comp, d_input, out, false); });
 }
 
 int bsq_device_decompress(const bsq_device_packed_t *packed, float *d_dst, uint32_t dst_num_elements) {
