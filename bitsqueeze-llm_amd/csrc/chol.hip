@@ -368,9 +368,20 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
         if (wave == 0) __builtin_amdgcn_s_setprio(3);  // its loads and the factorisation are the critical path
         {
             const int lane = opaque(static_cast<int>(threadIdx.x)) & 63, kq = lane >> 4, cc = lane & 15;
+            // waves 0, 4, 8, 12 load first: their tiles (block columns 0, 1) go to
+            // LDS before P0; the other waves issue the loads of their held
+            // tiles after P0, so those do not delay block 0 and stay in flight
+            // across the LDS-only barriers while wave 0 factors block 0 (each
+            // wave passes one barrier here)
+            if ((wave & 3) != 0) lds_barrier();  // P0
+#pragma unroll
+            for (int m = 0; m < SLOTS; ++m)
+                acc[m] = (tJ[m] < 0) ? f64x4{0.0, 0.0, 0.0, 0.0}  // uniform
+                                     : load_tile(G, k, tI[m], tJ[m], shift, kq, cc);
             if (attempt == 0 && wave == 0) {
                 // breakdown scale max |G_ii|, for wave 0 (tiny) and, through
-                // LDS, the others (the shift of a restart)
+                // LDS, the others (the shift of a restart); issued after the
+                // tile loads, so both memory round trips overlap
                 double dm = 0.0;
 #pragma unroll
                 for (int m = 0; m < (KP + 63) / 64; ++m) {
@@ -383,16 +394,6 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
                 tiny = (dmax > 0.0 ? dmax : 1.0) * 1e-15;
                 if (lane == 0) red[0] = dm;
             }
-            // waves 0, 4, 8, 12 load first: their tiles (block columns 0, 1) go to
-            // LDS before P0; the other waves issue the loads of their held
-            // tiles after P0, so those do not delay block 0 and stay in flight
-            // across the LDS-only barriers while wave 0 factors block 0 (each
-            // wave passes one barrier here)
-            if ((wave & 3) != 0) lds_barrier();  // P0
-#pragma unroll
-            for (int m = 0; m < SLOTS; ++m)
-                acc[m] = (tJ[m] < 0) ? f64x4{0.0, 0.0, 0.0, 0.0}  // uniform
-                                     : load_tile(G, k, tI[m], tJ[m], shift, kq, cc);
             if ((wave & 3) == 0) {
 #pragma unroll
                 for (int m = 0; m < SLOTS; ++m) {
