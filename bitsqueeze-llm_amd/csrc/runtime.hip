@@ -310,8 +310,9 @@ struct KernelTimer {
     void begin(hipStream_t st) {
         if (2 * used + 2 > ev.size()) {
             hipEvent_t a = nullptr, b = nullptr;
-            BSQ_HIP(hipEventCreate(&a));
-            if (hipEventCreate(&b) != hipSuccess) {
+            // no system-scope fence: these only time kernels on this device
+            BSQ_HIP(hipEventCreateWithFlags(&a, hipEventDisableSystemFence));
+            if (hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
                 (void)hipEventDestroy(a);
                 fail("kernel timer: hipEventCreate failed");
             }
