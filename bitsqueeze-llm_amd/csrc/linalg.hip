@@ -1045,12 +1045,12 @@ void launch_sytrd_blocked(const double *G, int k, double *d, double *e, double *
 // ---------------------------------------------------------------------------
 // Row splits of the Gram: at most one workgroup per CU over all lower tiles
 // (rounded down: one CU holding two workgroups would double the kernel's
-// time), at least 256 rows each (fewer partial matrices to sum).
+// time), at least 128 rows each (fewer partial matrices to sum).
 int gram_splits(int M, int k) {
     const int nt = static_cast<int>(ceil_div(k, kGramTile));
     const int tiles = nt * (nt + 1) / 2;
     const int splits = cu_count() / tiles;
-    return std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 256))));
+    return std::max(1, std::min(splits, static_cast<int>(ceil_div(M, 128))));
 }
 
 uint64_t gram_workspace_bytes(int M, int k) {
