@@ -9,15 +9,16 @@ matrix that is already in HBM; `value` is GB/s of FP32 input
 roofline figure of the dominant kernel and the reference's CPU codec timed on
 this host.
 
-Dominant kernel: on the SVD workloads, the FP32-MFMA GEMM that touches the
-full matrix; the one timed is the low-rank reconstruction
-U diag(S) V^T (gemm_dma_kernel<false, true, true, 128>), bracketed with HIP
-events on the runtime stream inside the timed steps (2 * rows * cols * rank
-flops per launch, twice per step).  On the direct workloads, the NF4 / NF4_DQ
-encode of the full matrix (read 4N bytes, write the section), timed with HIP
-events on the runtime stream after the timed steps.  `traffic` is read from
-the committed rocprofv3 --pmc summary for that kernel and workload, when one
-exists.
+Dominant kernel: on the SVD workloads, the FP32-MFMA GEMMs that touch the
+full matrix (the range finder's 2 + 2 it products and the low-rank
+reconstructions, 2 * rows * cols * rank flops each); on the direct
+workloads, the HBM-bound stage with the largest time per step (outlier
+separation, direct encode, error top-k or direct decode), at its
+algorithmic bytes.  Every one of them is bracketed with HIP events on the
+runtime stream inside the timed steps (bsq_kernel_timer_*).  `traffic` is
+the HBM bytes per launch of that class from the committed rocprofv3 --pmc
+summary of the workload, used only when the summary's recorded source hash
+equals the hash of the kernel sources this run was built from.
 
     python bench.py --calibrate-copy   # also launches the plain copy kernel
                                        # (for rocprofv3 --pmc calibration runs)
@@ -47,15 +48,27 @@ METRIC = "compress+decompress GB/s (FP32 in) at 4096×11008; % HBM/MFMA roofline
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
-# name -> (rows, cols, outlier ratio, error ratio, svd_ranks, svd_niters, uv, s, direct, generator)
+# name -> (rows, cols, outlier ratio, error ratio, svd_ranks, svd_niters, uv, s, direct, generator, input)
+# generator: "normal", "outlier_cols", or ("lowrank", rank, decay, noise std, outlier columns, their scale)
+HEADLINE_GEN = ("lowrank", 512, 1.2, 0.01, 8, 50.0)
 WORKLOADS = {
     # BASELINE headline: 4096x11008 low-rank + noise + outlier columns with config-4 knobs
-    "headline": (4096, 11008, 0.005, 0.01, 256, 2, B.NF4, B.QUANT_NONE, B.QUANT_NONE, "lowrank"),
+    "headline": (4096, 11008, 0.005, 0.01, 256, 2, B.NF4, B.QUANT_NONE, B.QUANT_NONE, HEADLINE_GEN, "device"),
     # the same matrix through the direct path (NF4_DQ + outlier + error top-k)
-    "direct_full": (4096, 11008, 0.005, 0.01, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4_DQ, "lowrank"),
-    "supplement": (4096, 11008, 0.0, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, "normal"),
-    "c1": (2048, 4096, 0.0, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, "normal"),
-    "c2": (4096, 4096, 0.005, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4_DQ, "outlier_cols"),
+    "direct_full": (4096, 11008, 0.005, 0.01, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4_DQ, HEADLINE_GEN, "device"),
+    "supplement": (4096, 11008, 0.0, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, "normal", "device"),
+    "c1": (2048, 4096, 0.0, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, "normal", "device"),
+    "c2": (4096, 4096, 0.005, 0.0, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4_DQ, "outlier_cols", "device"),
+    # SVD-only, FP32 factors: rank-512 spectrum i^-1.2 + noise 0.01, q = 128, it = 2
+    "c3": (4096, 11008, 0.0, 0.0, 128, 2, B.QUANT_NONE, B.QUANT_NONE, B.QUANT_NONE,
+           ("lowrank", 512, 1.2, 0.01, 0, 0.0), "device"),
+    # full pipeline: rank-512 spectrum i^-1.0 + noise 0.01 + 8 columns x50, q = 256, it = 2, UV NF4
+    "c4": (8192, 4096, 0.005, 0.01, 256, 2, B.NF4, B.QUANT_NONE, B.QUANT_NONE,
+           ("lowrank", 512, 1.0, 0.01, 8, 50.0), "device"),
+    # large full pipeline: rank-1024 spectrum i^-0.8 + noise 0.02 + 32 columns x80, q = 512, it = 3,
+    # UV NF4_DQ, HOST input
+    "c5": (16384, 14336, 0.002, 0.005, 512, 3, B.NF4_DQ, B.QUANT_NONE, B.QUANT_NONE,
+           ("lowrank", 1024, 0.8, 0.02, 32, 80.0), "host"),
 }
 
 
@@ -67,14 +80,15 @@ def make_input(rows, cols, gen, seed=0):
         x = rng.standard_normal((rows, cols), dtype=np.float32)
         x[:, np.random.default_rng(1).permutation(cols)[:16]] *= 60.0
         return x
-    # low-rank A diag(sigma) B^T (rank 512, sigma_i = i^-1.2) + N(0, 0.01^2) + 8 columns x50
-    r = 512
+    # low-rank A diag(sigma) B^T (sigma_i = i^-decay) + N(0, noise^2) + outlier columns
+    _, r, decay, noise, n_out, scale = gen
     A = rng.standard_normal((rows, r), dtype=np.float32)
     Bm = np.random.default_rng(seed + 1).standard_normal((cols, r), dtype=np.float32)
-    sig = (np.arange(1, r + 1, dtype=np.float32) ** np.float32(-1.2)).astype(np.float32)
+    sig = (np.arange(1, r + 1, dtype=np.float32) ** np.float32(-decay)).astype(np.float32)
     x = (A * sig[None, :]) @ Bm.T
-    x += np.float32(0.01) * np.random.default_rng(seed + 2).standard_normal((rows, cols), dtype=np.float32)
-    x[:, np.random.default_rng(seed + 3).permutation(cols)[:8]] *= 50.0
+    x += np.float32(noise) * np.random.default_rng(seed + 2).standard_normal((rows, cols), dtype=np.float32)
+    if n_out:
+        x[:, np.random.default_rng(seed + 3).permutation(cols)[:n_out]] *= np.float32(scale)
     return np.ascontiguousarray(x, np.float32)
 
 
@@ -90,46 +104,26 @@ def packed_payload_bytes(p: B.DevicePacked, err_present: bool) -> int:
     return total
 
 
-def time_dominant_kernel(wl, rows, cols, dsrc, stream, reps=20):
-    """Average duration (HIP events on the runtime stream) and algorithmic
-    bytes of the direct path's NF4/NF4_DQ encode of the full matrix, the
-    kernel that carries the direct-path traffic (read 4N, write the section)."""
-    _, _, ro, re, svd, _, uv, s, direct, _ = wl
-    n = rows * cols
-    method = direct if direct != B.QUANT_NONE else B.NF4
-    nb = (n + 63) // 64
-    scales_f = B.DeviceBuffer(nb * 4)
-    scales_u = B.DeviceBuffer(nb)
-    dq = B.DeviceBuffer(4)
-    codes = B.DeviceBuffer((n + 1) // 2)
+def abi_leg(src, ddst, n, wl, reps=5):
+    """Wall clock of the reference ABI calls bitsqz_llm_compress (host packed
+    object: includes the payload D2H) + bitsqz_llm_decompress (includes the
+    payload H2D); returns (GB/s of FP32 input, ms per step).  `src` is the
+    device buffer, or for a HOST-input workload the host matrix (the compress
+    runtime is re-initialised for HOST input, so its H2D is inside the call)."""
     L = B.lib()
-    for _ in range(3):
-        B.check(L.bsq_quant_compress(dsrc.ptr, n, method, scales_f.ptr, scales_u.ptr, dq.ptr, codes.ptr, stream),
-                "quant")
-    e0, e1 = B.Event(), B.Event()
-    e0.record(stream)
-    for _ in range(reps):
-        B.check(L.bsq_quant_compress(dsrc.ptr, n, method, scales_f.ptr, scales_u.ptr, dq.ptr, codes.ptr, stream),
-                "quant")
-    e1.record(stream)
-    ms = e0.elapsed_ms(e1) / reps
-    section = (nb * 4 if method == B.NF4 else nb) + (n + 1) // 2
-    alg_bytes = 4 * n + section
-    name = "quant_encode_kernel<NF4>" if method == B.NF4 else "dq_gmax_kernel + quant_encode_kernel<NF4_DQ>"
-    return name, ms, alg_bytes
-
-
-def abi_leg(dsrc, ddst, n, reps=5):
-    """Wall clock of the reference ABI calls bitsqz_llm_compress (device input,
-    host packed object: includes the payload D2H) + bitsqz_llm_decompress
-    (includes the payload H2D); returns (GB/s of FP32 input, ms per step)."""
-    L = B.lib()
+    rows, cols, ro, rerr, svd, nit, uv, s, direct, _, loc = wl
+    if loc == "host":
+        B.compress_release()
+        B.check(B.compress_initialize(rows, cols, ro, rerr, svd, nit, uv, s, direct, B.INPUT_HOST), "compress init")
+        src_ptr = src.ctypes.data_as(C.c_void_p)
+    else:
+        src_ptr = src.ptr
     times = []
     for i in range(reps + 1):
         out = C.POINTER(B.PackedHeader)()
         prof = B.Profile()
         t0 = time.perf_counter()
-        B.check(L.bsq_compress(dsrc.ptr, C.byref(out), C.byref(prof)), "bitsqz_llm_compress")
+        B.check(L.bsq_compress(src_ptr, C.byref(out), C.byref(prof)), "bitsqz_llm_compress")
         B.check(L.bsq_decompress(C.cast(out, C.c_void_p), ddst.ptr, n), "bitsqz_llm_decompress")
         dt = time.perf_counter() - t0
         L.bsq_free(C.cast(out, C.c_void_p))
@@ -139,15 +133,39 @@ def abi_leg(dsrc, ddst, n, reps=5):
     return 4.0 * n / (ms * 1e-3) / 1e9, ms
 
 
-def committed_traffic(kernel_tag: str, workload: str):
-    """HBM bytes per launch of `kernel_tag` at `workload` from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated),
-    or None when no such summary exists."""
-    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_{workload}_pmc.md")
+def sources_sha256() -> str:
+    """SHA-256 over the kernel and runtime sources, the public headers and the
+    build script (file names and contents, in name order): the identity of
+    the code a profile summary was collected from."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = []
+    for d, exts in ((os.path.join(PKG, "csrc"), (".hip", ".hpp")), (os.path.join(ROOT, "include"), (".h", ".hpp"))):
+        files += [os.path.join(d, f) for f in sorted(os.listdir(d)) if f.endswith(exts)]
+    files.append(os.path.join(PKG, "build.py"))
+    for f in files:
+        h.update(os.path.relpath(f, ROOT).encode())
+        h.update(open(f, "rb").read())
+    return h.hexdigest()
+
+
+def committed_traffic(workload: str, cls: str):
+    """HBM bytes per launch of timing class `cls` at `workload`
+    (FETCH_SIZE + WRITE_SIZE of every kernel the class launches, each
+    calibrated against the copy kernel), from profiles/<workload>_pmc.md when
+    that summary was collected from these exact sources; else None and why."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_pmc.md")
     if not os.path.exists(path):
-        return None
-    m = re.search(r"^traffic_bytes_per_launch\s*=\s*(\d+)", open(path).read(), re.M)
-    return int(m.group(1)) if m else None
+        return None, "no pmc summary for this workload"
+    text = open(path).read()
+    m = re.search(r"^sources_sha256\s*=\s*([0-9a-f]{64})", text, re.M)
+    if not m or m.group(1) != sources_sha256():
+        return None, "pmc summary collected from other sources"
+    m = re.search(r"^traffic_bytes_per_launch\[" + re.escape(cls) + r"\]\s*=\s*(\d+)", text, re.M)
+    if not m:
+        return None, f"pmc summary has no {cls} class"
+    return int(m.group(1)), os.path.relpath(path, ROOT)
 
 
 def roofline_time_ms(rows, cols, svd, nit, q, err_on, payload_bytes):
@@ -193,7 +211,9 @@ def cpu_baseline(x, direct, reps=5):
     nproc, model, sockets = host_cpu_info()
     want = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc
     ref_so = os.path.join(ROOT, "oracle", "_ref", "libref_nf4.so")
-    sample = np.ascontiguousarray(x, np.float32)
+    # bounded sample: at most the headline matrix's bytes (the first rows)
+    cap_rows = max(1, min(x.shape[0], (4096 * 11008) // x.shape[1]))
+    sample = np.ascontiguousarray(x[:cap_rows], np.float32)
     n = sample.size
     nb, nc = (n + 63) // 64, (n + 1) // 2
     out = np.empty(n, np.float32)
@@ -259,9 +279,10 @@ def cpu_baseline(x, direct, reps=5):
     label = "NF4" if method == B.NF4 else "NF4_DQ"
     a = runs["all"]
     return {"value": a["gbps_fp32_in"], "unit": "GB/s", "cores": a["threads"], "kind": kind,
-            "sample": f"legacy {label} compress and decompress of the full {x.shape[0]}x{x.shape[1]} matrix "
-                      f"({4 * n} bytes in), 1 warmup + median of {reps} each; the reference has no CPU "
-                      f"top-k / SVD path",
+            "sample": f"legacy {label} compress and decompress of "
+                      f"{'the full' if cap_rows == x.shape[0] else f'the first {cap_rows} rows of the'} "
+                      f"{x.shape[0]}x{x.shape[1]} matrix ({4 * n} bytes in), 1 warmup + median of {reps} each; "
+                      f"the reference has no CPU top-k / SVD path",
             "compress_ms": a["compress_ms"], "decompress_ms": a["decompress_ms"],
             "one_thread": runs["one"], "nproc": nproc, "cpu_model": model, "sockets": sockets}
 
@@ -420,17 +441,18 @@ def main():
         return
 
     wl = WORKLOADS[args.workload]
-    rows, cols, ro, re, svd, nit, uv, s, direct, gen = wl
+    rows, cols, ro, rerr, svd, nit, uv, s, direct, gen, loc = wl
     x = make_input(rows, cols, gen)
     print(f"bench: workload={args.workload} {rows}x{cols} generated", file=sys.stderr, flush=True)
     B.compress_release()
     B.decompress_release()
-    B.check(B.compress_initialize(rows, cols, ro, re, svd, nit, uv, s, direct, B.INPUT_DEVICE), "compress init")
+    B.check(B.compress_initialize(rows, cols, ro, rerr, svd, nit, uv, s, direct, B.INPUT_DEVICE), "compress init")
     q = max(1, min(svd, rows, cols)) if svd >= 1 else -1
-    B.check(B.decompress_initialize(rows, cols, ro, re, q, uv, s, direct), "decompress init")
+    B.check(B.decompress_initialize(rows, cols, ro, rerr, q, uv, s, direct), "decompress init")
     dsrc = B.DeviceBuffer.from_array(x)
     ddst = B.DeviceBuffer(x.nbytes)
     n = rows * cols
+    stream = B.runtime_stream()
 
     def step():
         p = B.device_compress(dsrc)
@@ -440,8 +462,6 @@ def main():
     for _ in range(args.warmup):
         p = step()
     B.device_synchronize()
-    if svd >= 1:
-        B.kernel_timer_start()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         p = step()
@@ -450,48 +470,111 @@ def main():
     ms_per_step = dt / args.steps * 1e3
     value = 4.0 * n * args.steps / dt / 1e9
     print(f"bench: timed {args.steps} steps, {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
+    # the same steps again with every timed class bracketed by HIP events on
+    # the runtime stream (each event record idles the queue for a few
+    # microseconds, so these steps are kept out of `value`)
+    B.kernel_timer_start()
+    for _ in range(args.steps):
+        p = step()
+    B.device_synchronize()
+    B.kernel_timer_stop()
+    timers = {name: B.kernel_timer_read(cls) for name, cls in (
+        ("reconstruct", B.TIMER_RECONSTRUCT), ("range_finder", B.TIMER_RANGE_FINDER),
+        ("topk_outlier", B.TIMER_TOPK_OUTLIER), ("topk_error", B.TIMER_TOPK_ERROR),
+        ("direct_encode", B.TIMER_DIRECT_ENCODE), ("direct_decode", B.TIMER_DIRECT_DECODE))}
     # correctness spot check of the last step against the input (reconstruction error)
     out = ddst.download(np.float32, n).reshape(rows, cols)
     rel = float(np.linalg.norm(out - x) / max(np.linalg.norm(x), 1e-30))
 
-    stream = B.runtime_stream()
+    # algorithmic work per launch of each timed class
+    err_present = bool(p.header.flags & 4)
+    ko = B.topk_num_columns(cols, ro) if ro > 0 else 0
+    ke = B.topk_num_columns(cols, rerr) if rerr > 0 else 0
+    sec = p.header.section_direct
+    p_dir = sec.size - 48 if sec.storage == 2 else 0  # scales + codes of a quantised direct section
+    alg = {"topk_outlier": 4 * n + 6 * rows * ko,
+           "topk_error": 4 * n + p_dir + 6 * rows * ke,
+           "direct_encode": 4 * n + p_dir,
+           "direct_decode": p_dir + 6 * rows * (ko + (ke if err_present else 0)) + 4 * n}
+    by_class = {}
+    for name, (ms, cnt) in timers.items():
+        if not cnt:
+            continue
+        avg = ms / cnt
+        e = {"launches": cnt, "per_step": round(cnt / args.steps, 3), "avg_ms": round(avg, 5),
+             "ms_per_step": round(ms / args.steps, 5)}
+        if name in alg:
+            gbs = alg[name] / (avg * 1e-3) / 1e9
+            e.update({"alg_bytes": alg[name], "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        else:
+            tf = 2.0 * n * q / (avg * 1e-3) / 1e12
+            e.update({"alg_flops": 2.0 * n * q, "tflops": round(tf, 2), "frac_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+        by_class[name] = e
+
     if svd >= 1:
         # the dominant kernel class: every GEMM over the m x n matrix (the
         # range finder's 2 + 2 it products and the reconstructions), each
         # 2 m n q flops, timed live with HIP events on the runtime's stream
-        B.kernel_timer_stop()
-        rec_ms, rec_n = B.kernel_timer_read(B.TIMER_RECONSTRUCT)
-        rf_ms, rf_n = B.kernel_timer_read(B.TIMER_RANGE_FINDER)
+        (rec_ms, rec_n), (rf_ms, rf_n) = timers["reconstruct"], timers["range_finder"]
         launches = rec_n + rf_n
         kms = (rec_ms + rf_ms) / max(launches, 1)
         kflops = 2.0 * rows * cols * q
         achieved = kflops / (kms * 1e-3) / 1e12
-        tflops = lambda ms, n: round(kflops * n / (ms * 1e-3) / 1e12, 2) if n else None
+        traffic, tsrc = committed_traffic(args.workload, "gemm_mxn")
         roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-                    "traffic": committed_traffic("gemm_mxn", args.workload),
-                    "kernel": "gemm_dma_kernel: the FP32-MFMA GEMMs over the m x n matrix "
-                              "(range finder A_w B / A_w^T B with split-K reduce, and U diag(S) V^T)",
-                    "avg_ms": round(kms, 5), "launches": launches, "alg_flops": kflops,
-                    "by_class": {"range_finder": {"launches": rf_n, "avg_ms": round(rf_ms / max(rf_n, 1), 5),
-                                                  "tflops": tflops(rf_ms, rf_n)},
-                                 "reconstruct": {"launches": rec_n, "avg_ms": round(rec_ms / max(rec_n, 1), 5),
-                                                 "tflops": tflops(rec_ms, rec_n)}}}
+                    "traffic": traffic, "traffic_source": tsrc,
+                    "kernel": "the FP32-MFMA GEMMs over the m x n matrix: range finder A_w B (gemm_dma_kernel, "
+                              "split-K + splitk_reduce_kernel) and A_w^T B (gemm_streamk_kernel + "
+                              "streamk_reduce_kernel), reconstructions U diag(S) V^T (gemm_dma_kernel RECON on "
+                              "the compress side, recon_q_kernel from the packed factors on the decompress side)",
+                    "avg_ms": round(kms, 5), "launches": launches, "alg_flops": kflops, "by_class": by_class}
     else:
-        kname, kms, kbytes = time_dominant_kernel(wl, rows, cols, dsrc, stream)
-        achieved = kbytes / (kms * 1e-3) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4),
-                    "traffic": committed_traffic("quant_encode", args.workload), "kernel": kname,
-                    "avg_ms": round(kms, 5), "alg_bytes": kbytes}
+        hbm = {k: v for k, v in by_class.items() if k in alg}
+        dom = max(hbm, key=lambda k: hbm[k]["ms_per_step"])
+        d = hbm[dom]
+        traffic, tsrc = committed_traffic(args.workload, dom)
+        kernels = {"topk_outlier": "topk_reg_kernel (outlier separation)",
+                   "topk_error": "topk_reg_kernel (error top-k of x - dequant)",
+                   "direct_encode": "quant_encode_kernel (+ rows_gmax_kernel for NF4_DQ)",
+                   "direct_decode": "quant_decode_rows_kernel / quant_decode_kernel"}
+        roofline = {"bound": "hbm", "achieved": d["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": d["frac_hbm"], "traffic": traffic, "traffic_source": tsrc,
+                    "kernel": f"{dom}: {kernels[dom]}", "avg_ms": d["avg_ms"], "alg_bytes": alg[dom],
+                    "by_class": by_class}
 
-    t_roof = roofline_time_ms(rows, cols, svd, nit, q, re > 0, packed_payload_bytes(p, bool(re > 0)))
+    t_roof = roofline_time_ms(rows, cols, svd, nit, q, rerr > 0, packed_payload_bytes(p, err_present))
     pipeline = {"t_roof_ms": round(t_roof, 4), "frac_of_roofline": round(t_roof / ms_per_step, 4)}
 
-    abi_gbs, abi_ms = abi_leg(dsrc, ddst, n)
+    host_step = None
+    if loc == "host":
+        # HOST input (BASELINE C5): the step includes the H2D copy of the
+        # matrix from page-locked host memory into the runtime's input buffer
+        hx = B.PinnedBuffer(n)
+        hx.array[:] = x.ravel()
+        for _ in range(2):
+            hx.copy_to_device_async(dsrc, stream)
+            step()
+        B.device_synchronize()
+        hk = max(3, args.steps // 2)
+        t0 = time.perf_counter()
+        for _ in range(hk):
+            hx.copy_to_device_async(dsrc, stream)
+            step()
+        B.device_synchronize()
+        hms = (time.perf_counter() - t0) / hk * 1e3
+        t_link = 4.0 * n / 64e9 * 1e3
+        host_step = {"value": round(4.0 * n / (hms * 1e-3) / 1e9, 3), "unit": "GB/s", "ms_per_step": round(hms, 4),
+                     "steps": hk, "t_roof_ms": round(t_roof + t_link, 4),
+                     "frac_of_roofline": round((t_roof + t_link) / hms, 4),
+                     "what": "H2D of the FP32 matrix from pinned host memory (on the runtime stream) + device "
+                             "compress + decompress; T_roof adds the matrix over a 64 GB/s host link"}
+        hx.free()
+
+    abi_gbs, abi_ms = abi_leg(x if loc == "host" else dsrc, ddst, n, wl)
     abi = {"value": round(abi_gbs, 3), "unit": "GB/s", "ms_per_step": round(abi_ms, 4),
-           "what": "bitsqz_llm_compress + bitsqz_llm_decompress wall clock (payload D2H / H2D included), "
-                   "median of 5"}
+           "what": "bitsqz_llm_compress + bitsqz_llm_decompress wall clock (payload D2H / H2D included"
+                   + (", and the HOST input's H2D" if loc == "host" else "") + "), median of 5"}
 
     if args.calibrate_copy:
         # known-size copy for rocprofv3 --pmc calibration (FETCH_SIZE / WRITE_SIZE per byte)
@@ -505,13 +588,15 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": args.workload, "rows": rows, "cols": cols, "outlier_topk_ratio": ro,
-                   "error_correction_topk_ratio": re, "svd_ranks": svd, "svd_niters": nit,
+                   "error_correction_topk_ratio": rerr, "svd_ranks": svd, "svd_niters": nit,
                    "svd_uv_format": uv, "svd_s_format": s, "quantization_only_format": direct,
                    "input": "device-resident", "rel_frobenius_error": round(rel, 6)},
         "roofline": roofline,
         "pipeline_roofline": pipeline,
         "abi_pcie_inclusive": abi,
     }
+    if host_step:
+        line["host_input_step"] = host_step
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(x, direct if svd < 1 else uv)
     B.compress_release()

@@ -122,6 +122,9 @@ def lib():
         "bsq_memcpy_d2h": (i32, [P, P, u64]),
         "bsq_memcpy_d2d": (i32, [P, P, u64]),
         "bsq_device_memset": (i32, [P, i32, u64]),
+        "bsq_host_malloc": (i32, [C.POINTER(P), u64]),
+        "bsq_host_free": (i32, [P]),
+        "bsq_memcpy_h2d_async": (i32, [P, P, u64, P]),
         "bsq_stream_synchronize": (i32, [P]),
         "bsq_event_create": (i32, [C.POINTER(P)]),
         "bsq_event_destroy": (i32, [P]),
@@ -214,11 +217,40 @@ class DeviceBuffer:
             pass
 
 
+class PinnedBuffer:
+    """hipHostMalloc'd (page-locked) host memory owned by Python, viewed as a
+    flat numpy array of `dtype`."""
+
+    def __init__(self, count: int, dtype=np.float32):
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(count) * self.dtype.itemsize
+        self.ptr = C.c_void_p()
+        check(lib().bsq_host_malloc(C.byref(self.ptr), max(self.nbytes, 1)), "hipHostMalloc")
+        buf = (C.c_char * max(self.nbytes, 1)).from_address(self.ptr.value)
+        self.array = np.frombuffer(buf, dtype=self.dtype, count=int(count))
+
+    def copy_to_device_async(self, dst: DeviceBuffer, stream=None):
+        check(lib().bsq_memcpy_h2d_async(dst.ptr, self.ptr, self.nbytes, stream), "H2D async")
+
+    def free(self):
+        if self.ptr and self.ptr.value:
+            self.array = None
+            lib().bsq_host_free(self.ptr)
+        self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 TIMER_RECONSTRUCT, TIMER_RANGE_FINDER = 0, 1
+TIMER_TOPK_OUTLIER, TIMER_TOPK_ERROR, TIMER_DIRECT_ENCODE, TIMER_DIRECT_DECODE = 2, 3, 4, 5
 
 
 def kernel_timer_start() -> None:
-    """Bracket every GEMM over the m x n matrix of the pipelines with HIP events."""
+    """Bracket the timed launch classes of the pipelines (TIMER_*) with HIP events."""
     check(lib().bsq_kernel_timer_start(), "kernel timer start")
 
 

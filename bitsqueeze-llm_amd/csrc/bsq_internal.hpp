@@ -137,10 +137,14 @@ struct TopkArgs {
     // (1 for an all-zero block), the per-row part of NF4_DQ's global scale
     float *row_gmax = nullptr;
     TopkSource source = TopkSource::Dense;
+    // written 0 by the kernel before anything else reads it (the compress
+    // flags word: the separation clears it instead of a memset launch)
+    uint32_t *flags_reset = nullptr;
 };
 // Returns true when row_gmax was requested and written (the register-resident
 // kernel on a Dense source with cols % 64 == 0); otherwise row_gmax is left
-// alone and the caller computes the global scale itself.
+// alone and the caller computes the global scale itself.  flags_reset is
+// honoured on every path (by a memset where the kernel does not take it).
 bool launch_topk_select(const TopkArgs &args, hipStream_t stream);
 // Largest k the single-workgroup LDS sort handles; larger k (up to the row
 // length) is sorted in bands of this many ranks.
@@ -206,15 +210,26 @@ void launch_recon_q(int method, const uint8_t *u_codes, const float *u_scales_f3
                     const float *v_dq, const float *S, int m, int n, int k, float *out, hipStream_t stream);
 
 // Instrumentation (off unless started through the ABI): HIP events bracket
-// every GEMM over the m x n matrix inside the pipelines, on the stream it runs
-// on.  Class 0: the low-rank reconstruction; class 1: the range finder's
-// products A_w B and A_w^T B (with their split-K reductions).
-enum GemmTimerClass { kTimeReconstruct = 0, kTimeRangeFinder = 1, kTimeClasses = 2 };
+// the launches of each class below inside the pipelines, on the stream they
+// run on.  0: the low-rank reconstruction GEMM; 1: the range finder's
+// products A_w B and A_w^T B (with their split-K / stream-K reductions);
+// 2: the outlier separation (top-k); 3: the error-correction top-k pass;
+// 4: the direct section's encode (with its NF4_DQ global-scale reduce);
+// 5: the direct section's decode (with the fused top-k scatter when it runs).
+enum GemmTimerClass {
+    kTimeReconstruct = 0,
+    kTimeRangeFinder = 1,
+    kTimeTopkOutlier = 2,
+    kTimeTopkError = 3,
+    kTimeDirectEncode = 4,
+    kTimeDirectDecode = 5,
+    kTimeClasses = 6
+};
 bool gemm_timer_on();
 void gemm_timer_begin(int cls, hipStream_t stream);
 void gemm_timer_end(int cls, hipStream_t stream);
 template <class F>
-void timed_gemm(int cls, hipStream_t stream, F &&launch) {
+void timed_launch(int cls, hipStream_t stream, F &&launch) {
     if (!gemm_timer_on()) {
         launch();
         return;

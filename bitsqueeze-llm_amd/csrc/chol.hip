@@ -28,6 +28,9 @@
 // same column space serves the range finder.
 #include "bsq_internal.hpp"
 
+#include <algorithm>
+#include <type_traits>
+
 namespace bsq {
 namespace {
 
@@ -546,13 +549,15 @@ __global__ __launch_bounds__(kCholThreads) void chol_blocked_kernel(const double
 // and 1 apply the lower-triangular LI_i.
 // MFMA operand lanes: A[r][q] and B[q][c] in lane 16 q + (r or c);
 // accumulator register u of lane l holds D[4 u + l / 16][l % 16].
-// Output B = L^{-T} (k x k FP32 row-major): B[c][r] = L^{-1}[r][c].
+// Output B = L^{-T} (k x k FP32 row-major): B[c][r] = L^{-1}[r][c]; or, with
+// B64, L^{-1} itself in FP64 (k x k row-major, zeros above the diagonal).
 constexpr int kTrinvThreads = 1024;
 
 template <int NB>
 __global__ __launch_bounds__(kTrinvThreads) void trinv_kernel(const double *__restrict__ Lin,
                                                               const double *__restrict__ LIin, int k,
-                                                              float *__restrict__ B, const int *__restrict__ run) {
+                                                              float *__restrict__ B, const int *__restrict__ run,
+                                                              double *__restrict__ B64 = nullptr) {
     if (run && run[0] == 0) return;  // uniform
     constexpr int KP = NB * 32;
     constexpr int PP = (NB > 1 ? 32 * (NB - 1) : 32) + 4;  // panel pitch (doubles): 2-way banks for the A reads
@@ -652,6 +657,13 @@ __global__ __launch_bounds__(kTrinvThreads) void trinv_kernel(const double *__re
             __syncthreads();
         }
         at0 += (d + 1) / 2;
+    }
+    if (B64) {  // uniform
+        for (int t = tid; t < 16 * k; t += kTrinvThreads) {
+            const int r = t >> 4, jj = t & 15, c = c0 + jj;
+            if (c < k) B64[static_cast<uint64_t>(r) * k + c] = (r >= c) ? X[r][jj] : 0.0;
+        }
+        return;
     }
     for (int jj = 0; jj < 16 && c0 + jj < k; ++jj) {
         float *brow = B + static_cast<uint64_t>(c0 + jj) * k;
@@ -855,6 +867,118 @@ __global__ __launch_bounds__(256) void ns_refine_kernel(const double *__restrict
     }
 }
 
+// C = alpha op(A) op(B) + (D ? D : 0), FP64, for the k x k blocks of the
+// two-level Cholesky below (M, N, K <= a few hundred).  op(A) is M x K (A
+// stored K x M when TA), op(B) is K x N (B stored N x K when TB).  One 32 x 32
+// tile of C per workgroup of 256 lanes, 2 x 2 outputs per lane, K staged
+// through LDS 16 at a time; entries outside the operands read as zero.
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void dgemm_small_kernel(int M, int N, int K, double alpha,
+                                                          const double *__restrict__ A, int lda,
+                                                          const double *__restrict__ B, int ldb,
+                                                          const double *__restrict__ D, int ldd,
+                                                          double *__restrict__ C, int ldc) {
+    __shared__ double As[16][33];  // As[kk][m]
+    __shared__ double Bs[16][33];  // Bs[kk][n]
+    const int tid = threadIdx.x, m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    const int tr = 2 * (tid >> 4), tc = 2 * (tid & 15);
+    double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        for (int t = tid; t < 512; t += 256) {
+            // element (kk, i) of the A and B chunks
+            const int kk = TA ? (t >> 5) : (t & 15), i = TA ? (t & 31) : (t >> 4);
+            const int gk = k0 + kk, gm = m0 + i, gn = n0 + i;
+            double a = 0.0, b = 0.0;
+            if (gk < K && gm < M) a = TA ? A[static_cast<uint64_t>(gk) * lda + gm] : A[static_cast<uint64_t>(gm) * lda + gk];
+            As[kk][i] = a;
+            const int kb = TB ? (t & 15) : (t >> 5), j = TB ? (t >> 4) : (t & 31);
+            const int gkb = k0 + kb, gnb = n0 + j;
+            if (gkb < K && gnb < N)
+                b = TB ? B[static_cast<uint64_t>(gnb) * ldb + gkb] : B[static_cast<uint64_t>(gkb) * ldb + gnb];
+            Bs[kb][j] = b;
+            (void)gn;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            const double a0 = As[kk][tr], a1 = As[kk][tr + 1], b0 = Bs[kk][tc], b1 = Bs[kk][tc + 1];
+            acc[0][0] = fma(a0, b0, acc[0][0]);
+            acc[0][1] = fma(a0, b1, acc[0][1]);
+            acc[1][0] = fma(a1, b0, acc[1][0]);
+            acc[1][1] = fma(a1, b1, acc[1][1]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const int r = m0 + tr + u, c = n0 + tc + v;
+            if (r < M && c < N) {
+                double x = alpha * acc[u][v];
+                if (D) x += D[static_cast<uint64_t>(r) * ldd + c];
+                C[static_cast<uint64_t>(r) * ldc + c] = x;
+            }
+        }
+}
+
+template <bool TA, bool TB>
+void dgemm_small(int M, int N, int K, double alpha, const double *A, int lda, const double *B, int ldb,
+                 const double *D, int ldd, double *C, int ldc, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(N, 32)), static_cast<unsigned>(ceil_div(M, 32)));
+    dgemm_small_kernel<TA, TB><<<grid, 256, 0, stream>>>(M, N, K, alpha, A, lda, B, ldb, D, ldd, C, ldc);
+    BSQ_HIP(hipGetLastError());
+}
+
+// dst (rows x cols, ld dld) = src (ld sld) in FP64, or zeros when src is
+// null; with dst32, the values rounded to FP32 go there instead.  (A kernel,
+// not a memset: the no-allocation SVD entry point may run under graph
+// capture.)
+__global__ void dcopy_block_kernel(const double *__restrict__ src, int sld, int rows, int cols,
+                                   double *__restrict__ dst, int dld, float *__restrict__ dst32) {
+    const uint64_t n = static_cast<uint64_t>(rows) * cols;
+    for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < n;
+         t += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(t / cols), c = static_cast<int>(t % cols);
+        const double v = src ? src[static_cast<uint64_t>(r) * sld + c] : 0.0;
+        if (dst32) dst32[static_cast<uint64_t>(r) * dld + c] = static_cast<float>(v);
+        else dst[static_cast<uint64_t>(r) * dld + c] = v;
+    }
+}
+
+void dcopy_block(const double *src, int sld, int rows, int cols, double *dst, int dld, float *dst32,
+                 hipStream_t stream) {
+    const uint64_t n = static_cast<uint64_t>(rows) * cols;
+    dcopy_block_kernel<<<static_cast<unsigned>(std::min<uint64_t>(ceil_div(n, 256), 1024)), 256, 0, stream>>>(
+        src, sld, rows, cols, dst, dld, dst32);
+    BSQ_HIP(hipGetLastError());
+}
+
+// G = L L^T and L^{-1} (FP64, k x k) on the blocked one-workgroup kernels
+// (k <= 256): the factorisation, then the triangular inverse.
+void chol_inverse_f64(const double *G, int k, double *Lbuf, double *Linv, int *status, hipStream_t stream) {
+    const int nb = static_cast<int>(ceil_div(k, 32));
+    auto go = [&](auto nbc) {
+        constexpr int NB = decltype(nbc)::value;
+        double *L = Lbuf, *LI = Lbuf + static_cast<uint64_t>(NB) * 32 * NB * 32;
+        chol_blocked_kernel<NB><<<1, kCholThreads, 0, stream>>>(G, k, L, LI, status, nullptr);
+        BSQ_HIP(hipGetLastError());
+        trinv_kernel<NB><<<static_cast<unsigned>(ceil_div(k, 16)), kTrinvThreads, 0, stream>>>(L, LI, k, nullptr,
+                                                                                               nullptr, Linv);
+        BSQ_HIP(hipGetLastError());
+    };
+    switch (nb) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 3: go(std::integral_constant<int, 3>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        case 5: go(std::integral_constant<int, 5>{}); break;
+        case 6: go(std::integral_constant<int, 6>{}); break;
+        case 7: go(std::integral_constant<int, 7>{}); break;
+        default: go(std::integral_constant<int, 8>{}); break;
+    }
+}
+
 }  // namespace
 
 // FP64 doubles needed by the L buffer of launch_chol_blocked and
@@ -898,6 +1022,55 @@ void launch_chol_solve(const double *G, int k, double *Lbuf, const float *X, int
         case 7: chol_solve<7>(G, k, Lbuf, X, M, Q, status, stream); break;
         default: chol_solve<8>(G, k, Lbuf, X, M, Q, status, stream); break;
     }
+}
+
+// Two-level Cholesky for 256 < k <= 512: with G = [[G11, G21^T], [G21, G22]]
+// split at k1 = 256,
+//   L11 = chol(G11);  L21 = G21 L11^{-T};  L22 = chol(G22 - L21 L21^T);
+//   L^{-1} = [[L11^{-1}, 0], [-L22^{-1} L21 L11^{-1}, L22^{-1}]],
+// both diagonal factorisations on the blocked one-workgroup kernels (each
+// shifted and restarted on its own block when it breaks down: L L^T then
+// equals G plus a non-negative diagonal, still a basis change of the same
+// column space for CholeskyQR), the off-diagonal products in FP64.  Linv gets
+// L^{-1} in FP32 (k x k row-major, zeros above the diagonal), as
+// launch_chol_inv writes it.  `work` holds chol_inv_2x2_work_doubles(k)
+// doubles; status[0] and status[1] count the two blocks' restarts.
+bool chol_inv_2x2_supported(int k) { return k > 256 && k <= 512; }
+
+uint64_t chol_inv_2x2_work_doubles(int k) {
+    const uint64_t k1 = 256, k2 = static_cast<uint64_t>(k) - k1;
+    return 2 * chol_blocked_buffer_doubles(256) + k1 * k1 * 2 + k2 * k2 * 2 + k2 * k1 * 3;
+}
+
+void launch_chol_inv_2x2(const double *G, int k, double *work, float *Linv, int *status, hipStream_t stream) {
+    BSQ_REQUIRE(chol_inv_2x2_supported(k) && G && work && Linv && status, "chol 2x2: bad arguments");
+    const int k1 = 256, k2 = k - k1;
+    double *w = work;
+    auto take = [&](uint64_t n) {
+        double *p = w;
+        w += n;
+        return p;
+    };
+    double *Lb1 = take(chol_blocked_buffer_doubles(256)), *Lb2 = take(chol_blocked_buffer_doubles(256));
+    double *G11 = take(static_cast<uint64_t>(k1) * k1), *Li1 = take(static_cast<uint64_t>(k1) * k1);
+    double *S = take(static_cast<uint64_t>(k2) * k2), *Li2 = take(static_cast<uint64_t>(k2) * k2);
+    double *L21 = take(static_cast<uint64_t>(k2) * k1), *T = take(static_cast<uint64_t>(k2) * k1);
+    double *I21 = take(static_cast<uint64_t>(k2) * k1);
+    const double *G21 = G + static_cast<uint64_t>(k1) * k, *G22 = G21 + k1;
+    dcopy_block(G, k, k1, k1, G11, k1, nullptr, stream);
+    chol_inverse_f64(G11, k1, Lb1, Li1, status, stream);
+    // L21 = G21 Li1^T;  S = G22 - L21 L21^T
+    dgemm_small<false, true>(k2, k1, k1, 1.0, G21, k, Li1, k1, nullptr, 0, L21, k1, stream);
+    dgemm_small<false, true>(k2, k2, k1, -1.0, L21, k1, L21, k1, G22, k, S, k2, stream);
+    chol_inverse_f64(S, k2, Lb2, Li2, status + 1, stream);
+    // (L^{-1})21 = -Li2 (L21 Li1)
+    dgemm_small<false, false>(k2, k1, k1, 1.0, L21, k1, Li1, k1, nullptr, 0, T, k1, stream);
+    dgemm_small<false, false>(k2, k1, k2, -1.0, Li2, k2, T, k1, nullptr, 0, I21, k1, stream);
+    // Linv = [[Li1, 0], [I21, Li2]] in FP32
+    dcopy_block(Li1, k1, k1, k1, nullptr, k, Linv, stream);
+    dcopy_block(nullptr, 0, k1, k2, nullptr, k, Linv + k1, stream);
+    dcopy_block(I21, k1, k2, k1, nullptr, k, Linv + static_cast<uint64_t>(k1) * k, stream);
+    dcopy_block(Li2, k2, k2, k2, nullptr, k, Linv + static_cast<uint64_t>(k1) * k + k1, stream);
 }
 
 // B such that Q B is orthonormal for the almost orthonormal Q with Gram G

@@ -317,12 +317,14 @@ __global__ __launch_bounds__(kBig) void chol_inv_kernel(const double *__restrict
 // d[0..k), e[0..k-1), reflector j stored in W[j+1.., j] (first entry 1),
 // tau[j].  One workgroup.
 // ---------------------------------------------------------------------------
+constexpr int kSytrdSegs = 8;  // matvec segments (rows of at most kBig / kSytrdSegs lanes each)
 __global__ __launch_bounds__(kBig) void sytrd_kernel(double *__restrict__ W, int k, double *__restrict__ d,
                                                       double *__restrict__ e, double *__restrict__ tau,
                                                       double *__restrict__ vp_ext) {
     extern __shared__ double sm_lds[];  // v[k], p[k], or vp_ext (global) when they do not fit
     double *sm = vp_ext ? vp_ext : sm_lds;
     double *v = sm, *p = sm + k;
+    __shared__ double part[kBig];  // the matvec's segment partial sums (segments x padded rows <= kBig)
     __shared__ double red[kBig / 64];
     const int tid = threadIdx.x;
     for (int j = 0; j + 2 < k; ++j) {
@@ -354,11 +356,45 @@ __global__ __launch_bounds__(kBig) void sytrd_kernel(double *__restrict__ W, int
         // store the reflector in column j below the diagonal
         for (int i = tid; i < n; i += kBig) W[static_cast<uint64_t>(j + 1 + i) * k + j] = v[i];
         if (t != 0.0) {
-            // p = t * A' v  (A' = trailing block, full symmetric storage)
-            for (int i = tid; i < n; i += kBig) {
-                double s = 0.0;
-                for (int c = 0; c < n; ++c) s = fma(W[static_cast<uint64_t>(j + 1 + c) * k + (j + 1 + i)], v[c], s);
-                p[i] = t * s;
+            // p = t * A' v  (A' = trailing block, full symmetric storage):
+            // lanes take consecutive rows i (coalesced reads of row c of A',
+            // which equals column c by symmetry); while the rows fit in the
+            // workgroup, its lanes also split the sum over c into `segs`
+            // contiguous segments (shorter dependent chains), combined through
+            // LDS
+            const int rows_pad = (n + 63) & ~63;  // whole waves per segment
+            if (rows_pad <= kBig) {
+                const int segs = min(kSytrdSegs, kBig / rows_pad);
+                const int seg = tid / rows_pad, i = tid - seg * rows_pad;
+                if (seg < segs && i < n) {
+                    // eight loads in flight per lane (the operand comes from L2)
+                    const int c0 = (n * seg) / segs, c1 = (n * (seg + 1)) / segs;
+                    const double *col = W + static_cast<uint64_t>(j + 1) * k + (j + 1 + i);
+                    double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+                    int c = c0;
+                    for (; c + 8 <= c1; c += 8) {
+                        double a[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) a[u] = col[static_cast<uint64_t>(c + u) * k];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) acc[u] = fma(a[u], v[c + u], acc[u]);
+                    }
+                    for (; c < c1; ++c) acc[0] = fma(col[static_cast<uint64_t>(c) * k], v[c], acc[0]);
+                    part[seg * rows_pad + i] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) +
+                                               ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+                }
+                __syncthreads();
+                for (int i2 = tid; i2 < n; i2 += kBig) {
+                    double s = 0.0;
+                    for (int g = 0; g < segs; ++g) s += part[g * rows_pad + i2];
+                    p[i2] = t * s;
+                }
+            } else {
+                for (int i = tid; i < n; i += kBig) {
+                    double s = 0.0;
+                    for (int c = 0; c < n; ++c) s = fma(W[static_cast<uint64_t>(j + 1 + c) * k + (j + 1 + i)], v[c], s);
+                    p[i] = t * s;
+                }
             }
             __syncthreads();
             double pv = 0.0;
@@ -367,12 +403,24 @@ __global__ __launch_bounds__(kBig) void sytrd_kernel(double *__restrict__ W, int
             const double half = 0.5 * t * pv;
             for (int i = tid; i < n; i += kBig) p[i] -= half * v[i];  // p <- w
             __syncthreads();
-            // A' -= v w^T + w v^T
-            const uint64_t nn = static_cast<uint64_t>(n) * n;
-            for (uint64_t q = tid; q < nn; q += kBig) {
-                const int r = static_cast<int>(q / n), c = static_cast<int>(q % n);
-                double *a = W + static_cast<uint64_t>(j + 1 + r) * k + (j + 1 + c);
-                *a -= v[r] * p[c] + p[r] * v[c];
+            // A' -= v w^T + w v^T: wave w takes rows r = w (mod 16), its lanes
+            // consecutive columns
+            // (eight 512-byte row pieces loaded before any is updated, so a
+            // wave keeps eight L2 round trips in flight instead of one)
+            const int lane = tid & 63, wave = tid >> 6;
+            for (int r = wave; r < n; r += kBig / 64) {
+                const double vr = v[r], pr = p[r];
+                double *arow = W + static_cast<uint64_t>(j + 1 + r) * k + (j + 1);
+                for (int c0 = lane; c0 < n; c0 += 64 * 8) {
+                    double a[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) a[u] = (c0 + 64 * u < n) ? arow[c0 + 64 * u] : 0.0;
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int c = c0 + 64 * u;
+                        if (c < n) arow[c] = a[u] - (vr * p[c] + pr * v[c]);
+                    }
+                }
             }
         }
         __syncthreads();

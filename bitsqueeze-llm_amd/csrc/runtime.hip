@@ -244,6 +244,7 @@ struct Runtime {
     float *d_residual = nullptr;  // input with outliers zeroed
     float *d_err = nullptr;       // residual - U S V^T (SVD path with error top-k)
     float *d_row_gmax = nullptr;  // per-row NF4_DQ block maxima from the outlier separation
+    hipEvent_t t_begin = nullptr, t_end = nullptr;  // bitsqz_llm_compress wall span (profile struct)
     Section sec[4];
     TopkBuf topk[2];
     Meta *meta = nullptr;
@@ -281,6 +282,8 @@ struct Runtime {
             if (e) (void)hipEventDestroy(e);
         for (auto &e : cev)
             if (e) (void)hipEventDestroy(e);
+        if (t_begin) (void)hipEventDestroy(t_begin);
+        if (t_end) (void)hipEventDestroy(t_end);
         if (stream) (void)hipStreamDestroy(stream);
         if (copy_stream) (void)hipStreamDestroy(copy_stream);
         *this = Runtime{};
@@ -466,6 +469,8 @@ void compress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int s
         if (sc.method != kMethodNone) sc.alloc_quant();
         if (direct == kMethodNF4DQ && rt.topk[TK_OUTLIER].capacity > 0) rt.d_row_gmax = dev_alloc<float>(rows);
     }
+    BSQ_HIP(hipEventCreate(&rt.t_begin));
+    BSQ_HIP(hipEventCreate(&rt.t_end));
     alloc_host_stage(rt);
     BSQ_HIP(hipStreamSynchronize(rt.stream));
     rt.initialized = true;
@@ -540,13 +545,14 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
     H.quantization_only_format = static_cast<quantization_method_t>(rt.direct_fmt);
     uint32_t flags = 0;
 
-    BSQ_HIP(hipMemsetAsync(&rt.meta->flags, 0, sizeof(uint32_t), st));
     mark(0);
 
     // outlier separation (topk_separation, src/bitsqz_llm.cu:1045-1056)
     const float *residual = d_in;
     bool have_row_gmax = false;
     TopkBuf &to = rt.topk[TK_OUTLIER];
+    TopkBuf &te = rt.topk[TK_ERROR];
+    const bool has_svd = rt.svd_ranks >= 1;
     if (to.capacity > 0) {
         TopkArgs a;
         a.a = d_in;
@@ -559,14 +565,15 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
         // the direct NF4_DQ section's global scale needs the largest block
         // absmax of the residual: the separation kernel reports it per row
         a.row_gmax = rt.d_row_gmax;
-        have_row_gmax = launch_topk_select(a, st);
+        a.flags_reset = &rt.meta->flags;  // cleared here instead of a memset launch
+        timed_launch(kTimeTopkOutlier, st, [&] { have_row_gmax = launch_topk_select(a, st); });
         residual = rt.d_residual;
         flags |= kFlagOutlier;
+    } else {
+        BSQ_HIP(hipMemsetAsync(&rt.meta->flags, 0, sizeof(uint32_t), st));
     }
     mark(1);
 
-    TopkBuf &te = rt.topk[TK_ERROR];
-    const bool has_svd = rt.svd_ranks >= 1;
     if (has_svd) {
         flags |= kFlagSvd;
         H.effective_rank = static_cast<int16_t>(rt.q);
@@ -592,7 +599,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
         mark(4);
         if (te.capacity > 0) {
             // reconstruct + subtract fused (src/bitsqz_llm.cu:1141-1163)
-            timed_gemm(kTimeReconstruct, st, [&] {
+            timed_launch(kTimeReconstruct, st, [&] {
                 launch_reconstruct(U.dense, S.dense, V.dense, rows, cols, rt.q, residual, rt.d_err, st);
             });
             mark(5);
@@ -604,7 +611,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
             a.indices = te.idx;
             a.values = te.val;
             a.flags = &rt.meta->flags;
-            launch_topk_select(a, st);
+            timed_launch(kTimeTopkError, st, [&] { launch_topk_select(a, st); });
         } else {
             mark(5);
         }
@@ -613,12 +620,14 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
         mark(2);
         if (D.method != kMethodNone) {
             D.dense = nullptr;
-            if (have_row_gmax && D.method == kMethodNF4DQ)
-                launch_quant_encode_dq_rows(residual, N, rt.d_row_gmax, rows, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
-                                            D.codes, &rt.meta->gmax, st);
-            else
-                launch_quant_encode(residual, N, D.method, D.scales_f32, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
-                                    D.codes, &rt.meta->gmax, st);
+            timed_launch(kTimeDirectEncode, st, [&] {
+                if (have_row_gmax && D.method == kMethodNF4DQ)
+                    launch_quant_encode_dq_rows(residual, N, rt.d_row_gmax, rows, D.scales_u8,
+                                                &rt.meta->dq[SEC_DIRECT], D.codes, &rt.meta->gmax, st);
+                else
+                    launch_quant_encode(residual, N, D.method, D.scales_f32, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
+                                        D.codes, &rt.meta->gmax, st);
+            });
             mark(3);
             mark(4);
             mark(5);
@@ -642,7 +651,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
                     a.scales_u8 = D.scales_u8;
                     a.dq = &rt.meta->dq[SEC_DIRECT];
                 }
-                launch_topk_select(a, st);
+                timed_launch(kTimeTopkError, st, [&] { launch_topk_select(a, st); });
             }
         } else {
             // FP32 direct section: the residual itself (copied when it is the
@@ -734,13 +743,13 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
             }
         }
         if (fused) {
-            timed_gemm(kTimeReconstruct, st, [&] {
+            timed_launch(kTimeReconstruct, st, [&] {
                 launch_recon_q(H.svd_uv_format, P.d_codes[SEC_U], P.d_scales_f32[SEC_U], P.d_scales_u8[SEC_U],
                                P.d_dq_scale[SEC_U], P.d_codes[SEC_V], P.d_scales_f32[SEC_V], P.d_scales_u8[SEC_V],
                                P.d_dq_scale[SEC_V], dense[SEC_S], rows, cols, q, d_dst, st);
             });
         } else {
-            timed_gemm(kTimeReconstruct, st,
+            timed_launch(kTimeReconstruct, st,
                        [&] { launch_reconstruct(dense[0], dense[1], dense[2], rows, cols, q, nullptr, d_dst, st); });
         }
     } else {
@@ -749,14 +758,19 @@ void decompress_device(Runtime &rt, const bsq_device_packed_t &P, const bool has
             BSQ_HIP(hipMemcpyAsync(d_dst, P.d_dense[SEC_DIRECT], N * 4, hipMemcpyDeviceToDevice, st));
         } else if (scatter && (ke > 0 || ko > 0) && quant_decode_rows_supported(rows, cols)) {
             // decode and both top-k sets in one pass over the rows
-            launch_quant_decode_rows(rows, cols, H.quantization_only_format, P.d_scales_f32[SEC_DIRECT],
-                                     P.d_scales_u8[SEC_DIRECT], P.d_dq_scale[SEC_DIRECT], P.d_codes[SEC_DIRECT],
-                                     P.d_topk_idx[1], P.d_topk_val[1], ke, err_gate, P.d_topk_idx[0],
-                                     P.d_topk_val[0], ko, d_dst, st);
+            timed_launch(kTimeDirectDecode, st, [&] {
+                launch_quant_decode_rows(rows, cols, H.quantization_only_format, P.d_scales_f32[SEC_DIRECT],
+                                         P.d_scales_u8[SEC_DIRECT], P.d_dq_scale[SEC_DIRECT], P.d_codes[SEC_DIRECT],
+                                         P.d_topk_idx[1], P.d_topk_val[1], ke, err_gate, P.d_topk_idx[0],
+                                         P.d_topk_val[0], ko, d_dst, st);
+            });
             return;
         } else {
-            launch_quant_decode(N, H.quantization_only_format, P.d_scales_f32[SEC_DIRECT], P.d_scales_u8[SEC_DIRECT],
-                                P.d_dq_scale[SEC_DIRECT], P.d_codes[SEC_DIRECT], d_dst, st);
+            timed_launch(kTimeDirectDecode, st, [&] {
+                launch_quant_decode(N, H.quantization_only_format, P.d_scales_f32[SEC_DIRECT],
+                                    P.d_scales_u8[SEC_DIRECT], P.d_dq_scale[SEC_DIRECT], P.d_codes[SEC_DIRECT], d_dst,
+                                    st);
+            });
         }
     }
     if (!scatter) return;
@@ -1269,10 +1283,8 @@ int bitsqz_llm_compress(const float *row_major_matrix_float_data, bitsqz_llm_arr
         Runtime &rt = g_comp;
         const uint64_t N = static_cast<uint64_t>(rt.rows) * rt.cols;
         const float *d_in = row_major_matrix_float_data;
-        hipEvent_t t_begin = nullptr, t_end = nullptr;
-        BSQ_HIP(hipEventCreate(&t_begin));
-        BSQ_HIP(hipEventCreate(&t_end));
-        try {
+        const hipEvent_t t_begin = rt.t_begin, t_end = rt.t_end;
+        {
             BSQ_HIP(hipEventRecord(t_begin, rt.stream));
             if (rt.input_location == BITSQZ_LLM_INPUT_HOST) {
                 BSQ_HIP(hipMemcpyAsync(rt.d_stage, row_major_matrix_float_data, N * 4, hipMemcpyHostToDevice,
@@ -1303,13 +1315,7 @@ int bitsqz_llm_compress(const float *row_major_matrix_float_data, bitsqz_llm_arr
                 profile->other_latency_ms = std::max(0.0, total - acc);
             }
             *out = buf;
-        } catch (...) {
-            (void)hipEventDestroy(t_begin);
-            (void)hipEventDestroy(t_end);
-            throw;
         }
-        (void)hipEventDestroy(t_begin);
-        (void)hipEventDestroy(t_end);
     });
 }
 
@@ -1588,6 +1594,14 @@ int bsq_memcpy_d2d(void *dst, const void *src, uint64_t bytes) {
 }
 int bsq_device_memset(void *dst, int value, uint64_t bytes) {
     return guarded([&] { BSQ_HIP(hipMemset(dst, value, bytes)); });
+}
+int bsq_host_malloc(void **ptr, uint64_t bytes) {
+    return guarded([&] { BSQ_HIP(hipHostMalloc(ptr, bytes, hipHostMallocDefault)); });
+}
+int bsq_host_free(void *ptr) { return guarded([&] { BSQ_HIP(hipHostFree(ptr)); }); }
+int bsq_memcpy_h2d_async(void *dst, const void *src, uint64_t bytes, void *stream) {
+    return guarded(
+        [&] { BSQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream))); });
 }
 int bsq_stream_synchronize(void *stream) {
     return guarded([&] { BSQ_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream))); });

@@ -33,6 +33,9 @@ uint64_t gram_workspace_bytes(int M, int k);
 void launch_gram(const float *X, int M, int k, int ld, double *G, double *workspace, hipStream_t stream,
                  double *rowsq = nullptr);
 void launch_chol_inv(const double *G, int k, double *W, float *Linv, int *status, double *ext, hipStream_t stream);
+bool chol_inv_2x2_supported(int k);
+uint64_t chol_inv_2x2_work_doubles(int k);
+void launch_chol_inv_2x2(const double *G, int k, double *work, float *Linv, int *status, hipStream_t stream);
 uint64_t chol_blocked_buffer_doubles(int k);
 bool chol_blocked_supported(int k);
 void launch_chol_blocked(const double *G, int k, double *Lbuf, float *B, int *status, hipStream_t stream,
@@ -276,7 +279,10 @@ void plan_buffers(SvdPlan &p, Get &&get) {
     get(p.csum, kColChunks * k);
     get(p.rowsq, k);
     get(p.csign, 2 * k);
-    get(p.scratch, 9 * k * k + 2 * k);
+    get(p.scratch, std::max<uint64_t>(9 * k * k + 2 * k,
+                                      chol_inv_2x2_supported(static_cast<int>(k))
+                                          ? chol_inv_2x2_work_doubles(static_cast<int>(k))
+                                          : 0));
     get(p.lambda, k);
     get(p.iscratch, 2 * k * k);
     get(p.status, 4);
@@ -351,7 +357,7 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
     }
     // X (Mw x k) = A_w * B (B is Nw x k)
     auto aw_times = [&](const float *Bm, float *out) {
-        timed_gemm(kTimeRangeFinder, st, [&] {
+        timed_launch(kTimeRangeFinder, st, [&] {
             if (!p->transposed) launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
                                             p->gemm_ws_bytes, st);
             else launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
@@ -360,7 +366,7 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
     };
     // Y (Nw x k) = A_w^T * B (B is Mw x k)
     auto awt_times = [&](const float *Bm, float *out) {
-        timed_gemm(kTimeRangeFinder, st, [&] {
+        timed_launch(kTimeRangeFinder, st, [&] {
             if (!p->transposed) launch_gemm(true, false, n, k, m, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
                                             p->gemm_ws_bytes, st);
             else launch_gemm(false, false, m, k, n, A, n, Bm, k, out, k, nullptr, nullptr, p->gemm_ws,
@@ -374,7 +380,10 @@ void svd_run(SvdPlan *p, const float *A, const float *sketch, uint64_t seed, flo
             launch_chol_solve(p->G, k, p->Lbuf, in, rows, out, p->status, st);
             return;
         }
-        launch_chol_inv(p->G, k, p->W, p->Linv, p->status, p->scratch, st);  // Linv holds L^{-1}
+        if (chol_inv_2x2_supported(k))  // Linv holds L^{-1}
+            launch_chol_inv_2x2(p->G, k, p->scratch, p->Linv, p->status, st);
+        else
+            launch_chol_inv(p->G, k, p->W, p->Linv, p->status, p->scratch, st);
         launch_gemm(false, true, rows, k, k, in, k, p->Linv, k, out, k, nullptr, nullptr, p->gemm_ws,
                     p->gemm_ws_bytes, st);
     };

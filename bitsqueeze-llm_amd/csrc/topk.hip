@@ -525,6 +525,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         sh.kt = 0;
         sh.kth = 0;
         sh.ncand = 0;
+        if (a.flags_reset && r == 0) *a.flags_reset = 0u;
     }
     float dq = 1.0f;
     if constexpr (SRC == TopkSource::DenseMinusNF4DQ) {
@@ -1010,12 +1011,17 @@ void launch_src(const TopkArgs &a, hipStream_t stream) {
 
 bool launch_topk_select(const TopkArgs &args, hipStream_t stream) {
     TopkArgs a = args;
-    const bool gmax = a.row_gmax && a.residual && a.source == TopkSource::Dense && a.cols % 64 == 0 &&
-                      reg_eligible(a);
+    const bool reg = a.k >= 1 && a.k <= kTopkMaxK && reg_eligible(a);
+    const bool gmax = a.row_gmax && a.residual && a.source == TopkSource::Dense && a.cols % 64 == 0 && reg;
     if (!gmax) a.row_gmax = nullptr;
     BSQ_REQUIRE(a.rows > 0 && a.cols > 0 && a.cols <= 65535 && a.rows <= 65535, "top-k: bad shape");
     BSQ_REQUIRE(a.k >= 1 && a.k <= a.cols, "top-k: k must be in [1, cols]");
     BSQ_REQUIRE(a.a && a.indices && a.values, "top-k: null pointer");
+    BSQ_REQUIRE(!(a.flags_reset && a.flags), "top-k: a pass that sets the flags word cannot also clear it");
+    if (a.flags_reset && !reg) {
+        BSQ_HIP(hipMemsetAsync(a.flags_reset, 0, sizeof(uint32_t), stream));
+        a.flags_reset = nullptr;
+    }
     switch (a.source) {
         case TopkSource::Dense: launch_src<TopkSource::Dense>(a, stream); break;
         case TopkSource::DenseMinusDense:

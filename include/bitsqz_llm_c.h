@@ -235,6 +235,12 @@ BSQ_API int bsq_memcpy_h2d(void *dst, const void *src, uint64_t bytes);
 BSQ_API int bsq_memcpy_d2h(void *dst, const void *src, uint64_t bytes);
 BSQ_API int bsq_memcpy_d2d(void *dst, const void *src, uint64_t bytes);
 BSQ_API int bsq_device_memset(void *dst, int value, uint64_t bytes);
+/* Pinned (page-locked) host memory, hipHostMalloc / hipHostFree, and an
+ * asynchronous host-to-device copy on a caller-chosen stream (null: the
+ * default stream). */
+BSQ_API int bsq_host_malloc(void **ptr, uint64_t bytes);
+BSQ_API int bsq_host_free(void *ptr);
+BSQ_API int bsq_memcpy_h2d_async(void *dst, const void *src, uint64_t bytes, void *stream);
 BSQ_API int bsq_stream_synchronize(void *stream);
 /* HIP events on a caller-chosen stream (timing without a GPU framework). */
 BSQ_API int bsq_event_create(void **event);
@@ -242,12 +248,15 @@ BSQ_API int bsq_event_destroy(void *event);
 BSQ_API int bsq_event_record(void *event, void *stream);
 BSQ_API int bsq_event_elapsed_ms(void *start, void *stop, float *ms);
 
-/* Instrumentation (no counterpart in the reference): while started, every
- * GEMM over the m x n matrix launched by the compress / decompress pipelines
- * is bracketed by HIP events on its own stream.  _stop waits for those events
+/* Instrumentation (no counterpart in the reference): while started, the
+ * launches of six classes inside the compress / decompress pipelines are
+ * bracketed by HIP events on their own stream.  _stop waits for those events
  * and returns the summed time and launch count of the low-rank reconstruction
- * GEMMs; _read then returns either class: 0 = reconstruction, 1 = the range
- * finder's products with the big matrix (split-K reductions included). */
+ * GEMMs; _read then returns any class: 0 = reconstruction GEMM, 1 = the range
+ * finder's products with the big matrix (split-K / stream-K reductions
+ * included), 2 = outlier separation top-k, 3 = error-correction top-k,
+ * 4 = direct-section encode (with the NF4_DQ global-scale reduce),
+ * 5 = direct-section decode (with the fused top-k scatter). */
 BSQ_API int bsq_kernel_timer_start(void);
 BSQ_API int bsq_kernel_timer_read(int timer_class, double *total_ms, int *launches);
 /* Plain device copy kernel (16 bytes per lane), the known-size reference for

@@ -240,3 +240,39 @@ def test_device_resident_direct_decode_fused_with_the_scatter(rows, cols, fmt, r
     assert dst.download(np.float32, rows * cols).reshape(rows, cols).tobytes() == exp_out.tobytes()
     B.compress_release()
     B.decompress_release()
+
+
+@pytest.mark.parametrize("fmt", [B.NF4, B.NF4_DQ])
+def test_direct_separation_keys_edge_rows(fmt):
+    """The quantised direct path with an outlier separation keeps only each
+    row's k-th largest composite key (no residual is written); the encode
+    and the error pass zero the selected entries of the input themselves.
+    Rows whose k-th entry is a NaN (fewer than k numbers: every number and the
+    lowest-column NaNs are separated), ties at the k-th magnitude (lower
+    columns win), infinities, all-zero and signed-zero rows give the oracle's
+    bytes and decode, through the ABI and the device-resident twin."""
+    rows, cols = 24, 512
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[0, :] = np.nan
+    x[0, rng.permutation(cols)[:10]] = rng.standard_normal(10).astype(np.float32)  # 10 numbers < k
+    x[1, :] = np.where(np.arange(cols) % 2 == 0, 1.0, -1.0).astype(np.float32)    # all tied
+    x[2, rng.permutation(cols)[:30]] = np.float32(np.inf)
+    x[2, 7] = -np.inf
+    x[3, :] = 0.0
+    x[4, :] = np.where(np.arange(cols) % 3 == 0, -0.0, 0.0).astype(np.float32)
+    x[5, 100:140] = np.float32(3.5)  # a tie run straddling the k-th rank
+    ro, re = 0.05, 0.1
+    assert O.topk_num_columns(cols, ro) == 26 and O.topk_num_columns(cols, re) == 51
+    data, out, _ = run_direct(x, ro, re, fmt)
+    exp_bytes, exp_out = oracle_direct(x, ro, re, fmt)
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+    src = B.DeviceBuffer.from_array(x)
+    dst = B.DeviceBuffer(rows * cols * 4)
+    packed = B.device_compress(src)
+    B.device_decompress(packed, dst, rows * cols)
+    B.device_synchronize()
+    assert dst.download(np.float32, rows * cols).reshape(rows, cols).tobytes() == exp_out.tobytes()
+    B.compress_release()
+    B.decompress_release()

@@ -94,6 +94,28 @@ def test_svd_matches_oracle_with_injected_sketch(m, n, q, it, decay):
     assert np.abs(U.astype(np.float64).T @ U - np.eye(k)).max() < 1e-4
 
 
+@pytest.mark.parametrize("m,n,q,r", [(1200, 700, 300, 120), (900, 2000, 512, 200), (600, 400, 257, 257)])
+def test_two_level_cholesky_low_rank_recovery(m, n, q, r):
+    """Ranks 257 .. 512 orthonormalise with the two-level Cholesky (the
+    256-rank blocked factorisation of the leading block and of the Schur
+    complement, FP64 products between them).  A rank-r input with r < q makes
+    both Gram blocks singular, so each block's factorisation restarts with a
+    diagonal shift; the basis still spans the input, so U S V^T reproduces it
+    and the signal part of U is orthonormal.  r = q = 257 leaves a one-column
+    second block."""
+    A = lowrank(m, n, r, 0.3, 0.0, seed=q + r)
+    U, S, V = B.svd_lowrank(A, q, 2)
+    assert U.shape == (m, q) and V.shape == (n, q)
+    assert np.all(np.diff(S) <= 0) and np.all(np.isfinite(U)) and np.all(np.isfinite(V))
+    assert rel(O.reconstruct(U, S, V), A) < 1e-5
+    rr = min(r, q)
+    Us = U[:, :rr].astype(np.float64)
+    assert np.abs(Us.T @ Us - np.eye(rr)).max() < 1e-4
+    Z = np.zeros((m, n), np.float32)
+    U, S, V = B.svd_lowrank(Z, q, 1)
+    assert np.all(S == 0) and np.all(np.isfinite(U)) and np.all(np.isfinite(V))
+
+
 def test_svd_config3_full_size():
     """BASELINE config 3 (4096 x 11008, rank-512 spectrum i^-1.2 + noise 0.01,
     q = 128, 2 power iterations) with an injected sketch."""
