@@ -203,16 +203,9 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     uint8_t *__restrict__ scales_u8, const uint32_t *__restrict__ gmax, float *__restrict__ dq_out,
     uint8_t *__restrict__ codes) {
     __shared__ Nf4Table tab;
-    nf4_table_build(tab);
     const uint64_t nchunks = ceil_div(n, 8);
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
-    float dq = 1.0f;
-    if constexpr (DQ) {
-        const float raw = dq_raw_from_gmax(*gmax);
-        dq = dq_effective(raw);
-        if (blockIdx.x == 0 && threadIdx.x == 0) *dq_out = raw;
-    }
-    __syncthreads();
+    float dq = 1.0f;  // NF4_DQ: set below, before the first encode
     // chunks of one iteration: loaded one iteration ahead (two register
     // sets), so the loads of iteration i + 1 are in flight while iteration i
     // is encoded
@@ -279,9 +272,20 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     const uint64_t step = static_cast<uint64_t>(kUnroll) * stride;
     float va[kUnroll][8], vb[kUnroll][8];
     uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads;
+    // the first two iterations' loads go out before the code table is built
+    // and the global scale read (neither feeds an address), so the table
+    // work and the barrier overlap the first memory round trip
     if (base < nchunks) load_it(base, va);
-    for (; base < nchunks; base += 2 * step) {  // uniform
-        if (base + step < nchunks) load_it(base + step, vb);
+    if (base + step < nchunks) load_it(base + step, vb);
+    nf4_table_build(tab);
+    if constexpr (DQ) {
+        const float raw = dq_raw_from_gmax(*gmax);
+        dq = dq_effective(raw);
+        if (blockIdx.x == 0 && threadIdx.x == 0) *dq_out = raw;
+    }
+    __syncthreads();
+    for (bool first = true; base < nchunks; base += 2 * step, first = false) {  // uniform
+        if (!first && base + step < nchunks) load_it(base + step, vb);
         encode_it(base, va);
         if (base + step >= nchunks) break;
         if (base + 2 * step < nchunks) load_it(base + 2 * step, va);
@@ -509,6 +513,7 @@ unsigned grid_for(uint64_t work_items, unsigned per_cu = 8) {
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 
 }  // namespace
 

@@ -91,6 +91,19 @@ def test_config4_full_pipeline():
 
 
 @pytest.mark.timeout(900)
+def test_config3_full_pipeline_fp32_factors():
+    """BASELINE C3 through the ABI at full size: 4096 x 11008, rank-512
+    spectrum i^-1.2 + noise 0.01, q = 128, 2 iterations, U / S / V stored as
+    FP32 sections, no top-k.  The sections equal the standalone SVD's factors
+    (which match the FP64 oracle to 1e-4), and the decode is their
+    reconstruction, byte for byte."""
+    x = lowrank(4096, 11008, 512, 1.2, 0.01, seed=0)
+    data, _, e = _full_pipeline(x, 0.0, 0.0, 128, 2, B.QUANT_NONE, B.QUANT_NONE, B.INPUT_DEVICE)
+    assert len(data) == 200 + 7733760
+    assert e < 0.2
+
+
+@pytest.mark.timeout(900)
 def test_headline_full_pipeline():
     """The headline workload: 4096 x 11008 with the C3 generator and 8 columns
     x50, C4's knobs (k_o = 55, k_e = 110, q = 256, it = 2, UV NF4)."""

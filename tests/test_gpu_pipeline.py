@@ -91,6 +91,30 @@ def test_config2_4096x4096_nf4dq_outliers():
     assert out.tobytes() == exp_out.tobytes()
 
 
+def test_direct_full_4096x11008_nf4dq_outlier_error():
+    """The benched direct workload at full size: the headline matrix (rank-512
+    spectrum i^-1.2 + noise 0.01, 8 columns x50) through the direct path with
+    NF4_DQ, outlier top-k 0.005 (55 per row) and error top-k 0.01 (110 per
+    row): packed bytes and decode equal the oracle's, through the ABI and the
+    device-resident twin."""
+    from _svdcase import lowrank, outlier_columns
+    x = outlier_columns(lowrank(4096, 11008, 512, 1.2, 0.01, seed=0), 8, 50.0)
+    rows, cols = x.shape
+    data, out, _ = run_direct(x, 0.005, 0.01, B.NF4_DQ)
+    exp_bytes, exp_out = oracle_direct(x, 0.005, 0.01, B.NF4_DQ)
+    assert len(data) == len(exp_bytes)
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+    src = B.DeviceBuffer.from_array(x)
+    dst = B.DeviceBuffer(rows * cols * 4)
+    packed = B.device_compress(src)
+    B.device_decompress(packed, dst, rows * cols)
+    B.device_synchronize()
+    assert dst.download(np.float32, rows * cols).reshape(rows, cols).tobytes() == exp_out.tobytes()
+    B.compress_release()
+    B.decompress_release()
+
+
 @pytest.mark.parametrize("rows,cols", [(48, 4096), (40, 1000), (16, 11008)])
 def test_nf4dq_global_scale_from_the_outlier_separation(rows, cols):
     """The direct NF4_DQ section's global scale comes from the outlier

@@ -89,7 +89,10 @@ def test_nf4_code_random_values():
     assert B.nf4_codes(v).tobytes() == O.nf4_codes(v).tobytes()
 
 
-@pytest.mark.parametrize("n", [1, 2, 63, 64, 65, 127, 1000, 4097, 100003])
+@pytest.mark.parametrize("n", [1, 2, 63, 64, 65, 127, 1000, 1023, 1024, 1025, 4097, 100003,
+                               # past one pass of the contiguous-load encode's grid (2048 workgroups x
+                               # 4 tiles of 1024 on 256 CUs), with a partial last tile and an odd count
+                               3 * 4 * 1024 * 2048 + 777])
 def test_nf4_partial_blocks(n):
     rng = np.random.default_rng(n)
     x = rng.standard_normal(n).astype(np.float32)

@@ -231,6 +231,49 @@ def test_svd_reconstruction_is_projection():
     assert np.allclose(O.reconstruct(U, S, V), proj, atol=1e-9)
 
 
+@pytest.mark.parametrize("shape", [(40, 60), (60, 40)])
+@pytest.mark.parametrize("it", [0, 1, 2])
+def test_svd_iteration_semantics_closed_form(shape, it):
+    """The oracle's range-finder basis spans orth((A_w A_w^T)^it A_w R), with
+    A_w = A for m >= n and A^T for m < n (svd_lowrank_cuda.cu:129-137,
+    284-386): its projector equals the one of that product formed directly in
+    float64, with no intermediate QR, on a spectrum mild enough that the
+    direct power is well conditioned.  The same check against it - 1 and
+    it + 1 iterations and against the sketch applied on the other side shows
+    the case tells those apart."""
+    m, n = shape
+    k, r = 8, 30
+    rng = np.random.default_rng(m * 7 + it)
+    a, _ = np.linalg.qr(rng.standard_normal((m, r)))
+    b, _ = np.linalg.qr(rng.standard_normal((n, r)))
+    A = (a * (0.85 ** np.arange(r))) @ b.T
+    transposed = m < n
+    Aw = A.T if transposed else A
+    R = rng.standard_normal((min(m, n), k))
+    U, S, V = O.svd_lowrank(A, k, it, R)
+    basis = V if transposed else U  # U_w = Q U_hat: the range-finder basis, in A_w's row space
+
+    def projector(Y):
+        Y = np.asarray(Y, np.float64)
+        return Y @ np.linalg.solve(Y.T @ Y, Y.T)
+
+    def direct(p):
+        Y = Aw @ R
+        for _ in range(p):
+            Y = Aw @ (Aw.T @ Y)
+        return projector(Y)
+
+    P = basis @ basis.T
+    assert np.linalg.norm(P - direct(it)) < 1e-9
+    for p in (it - 1, it + 1):
+        if p >= 0:
+            assert np.linalg.norm(P - direct(p)) > 1e-3
+    # the sketch on the other side: A_w^T R' spans a subspace of the other
+    # dimension; its row-space image A_w (A_w^T R') is a different subspace
+    Rw = rng.standard_normal((Aw.shape[0], k))
+    assert np.linalg.norm(P - projector(Aw @ (Aw.T @ Rw))) > 1e-3
+
+
 # ---------------------------------------------------------------- pipeline --
 def test_pipeline_direct_round_trip():
     rng = np.random.default_rng(11)
