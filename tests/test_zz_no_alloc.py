@@ -62,3 +62,63 @@ def test_noalloc_rejects_a_plan_above_its_scratch():
     ref = _svd("bsq_svd_lowrank", A, 16, 1)
     got = _svd("bsq_svd_lowrank_noalloc", A, 16, 1)
     assert all(a.tobytes() == b.tobytes() for a, b in zip(got, ref))
+
+
+def _hip():
+    import ctypes as C
+    h = C.CDLL("libamdhip64.so")
+    P = C.c_void_p
+    for name, args in (("hipStreamCreate", [C.POINTER(P)]), ("hipStreamDestroy", [P]),
+                       ("hipStreamSynchronize", [P]), ("hipStreamBeginCapture", [P, C.c_int]),
+                       ("hipStreamEndCapture", [P, C.POINTER(P)]),
+                       ("hipGraphInstantiate", [C.POINTER(P), P, P, P, C.c_size_t]),
+                       ("hipGraphLaunch", [P, P]), ("hipGraphExecDestroy", [P]), ("hipGraphDestroy", [P])):
+        getattr(h, name).restype = C.c_int
+        getattr(h, name).argtypes = args
+    return h
+
+
+def test_noalloc_captured_in_a_graph_and_replayed():
+    """The entry point's intended caller: one eager call (which looks up the
+    scratch array's device address), then the same call captured into a HIP
+    graph on a non-default stream, instantiated and replayed three times with
+    eager work of the allocating entry point and host synchronisations
+    between the replays; every replay's U, S, V equal the allocating entry
+    point's bit for bit (the built-in sketch is deterministic)."""
+    import ctypes as C
+    h = _hip()
+    m, n, q, it = 700, 1200, 64, 2
+    A = _lowrank(m, n, 128, 1.0, seed=77)
+    ref = _svd("bsq_svd_lowrank", A, q, it)
+    dA = B.DeviceBuffer.from_array(A)
+    k = q
+    dU, dS, dV = B.DeviceBuffer(m * k * 4), B.DeviceBuffer(k * 4), B.DeviceBuffer(n * k * 4)
+    s = C.c_void_p()
+    assert h.hipStreamCreate(C.byref(s)) == 0
+    call = lambda: B.lib().bsq_svd_lowrank_noalloc(dA.ptr, m, n, q, it, None, 1241, dU.ptr, dS.ptr, dV.ptr, s)
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        B.check(call(), "eager noalloc")
+        assert h.hipStreamSynchronize(s) == 0
+        assert h.hipStreamBeginCapture(s, 2) == 0  # relaxed capture mode
+        rc = call()
+        assert h.hipStreamEndCapture(s, C.byref(graph)) == 0
+        B.check(rc, "captured noalloc")
+        assert h.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        B2 = _lowrank(300, 500, 40, 1.2, seed=9)
+        for rep in range(3):
+            for buf in (dU, dS, dV):
+                buf.zero()
+            assert h.hipGraphLaunch(exe, s) == 0
+            assert h.hipStreamSynchronize(s) == 0
+            got = (dU.download(np.float32, m * k), dS.download(np.float32, k), dV.download(np.float32, n * k))
+            for a, b, name in zip(got, ref, "USV"):
+                assert a.tobytes() == b.tobytes(), f"replay {rep}: {name} differs"
+            _svd("bsq_svd_lowrank", B2, 16, 1)  # eager work between the replays
+    finally:
+        if exe.value:
+            h.hipGraphExecDestroy(exe)
+        if graph.value:
+            h.hipGraphDestroy(graph)
+        h.hipStreamSynchronize(s)
+        h.hipStreamDestroy(s)
