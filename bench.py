@@ -2,12 +2,18 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-A step is one device-resident compress (bsq_device_compress) followed by one
-device-resident decompress (bsq_device_decompress) of a synthetic FP32
-matrix that is already in HBM; `value` is GB/s of FP32 input
-(4*rows*cols*K / time of the K timed steps).  Prints one JSON line with the
-roofline figure of the dominant kernel and the reference's CPU codec timed on
-this host.
+A step is one device-resident compress followed by one device-resident
+decompress of a synthetic FP32 matrix that is already in HBM, on each of L
+lanes (bsq_lanes_roundtrip, --lanes, default 4): L independent runtime pairs
+on their own streams, each with its own copy of the matrix, so the one-CU
+stages of one matrix's randomised SVD run beside another's matrix-core GEMMs.
+`value` is GB/s of FP32 input (4*rows*cols*L*K / time of the K timed steps);
+`single_lane` gives the same pipeline one matrix at a time
+(bsq_device_compress + bsq_device_decompress on the process-global runtimes,
+the reference ABI's model).  Every lane's decode is checked byte for byte
+against the single-lane decode.  Prints one JSON line with the roofline
+figure of the dominant kernel and the reference's CPU codec timed on this
+host.  HOST-input workloads (c5) run single-lane.
 
 Dominant kernel: on the SVD workloads, the FP32-MFMA GEMMs that touch the
 full matrix (the range finder's 2 + 2 it products and the low-rank
@@ -428,6 +434,9 @@ def main():
     ap.add_argument("--workload", default="headline", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--lanes", type=int, default=4,
+                    help="matrices in flight per step on independent runtime lanes (bsq_lanes_*), each on its own "
+                         "stream; 1 = one matrix at a time through the process-global runtimes")
     ap.add_argument("--legacy", action="store_true",
                     help="measure the legacy formats' device codecs instead of the packed-object pipeline")
     args = ap.parse_args()
@@ -576,13 +585,62 @@ def main():
            "what": "bitsqz_llm_compress + bitsqz_llm_decompress wall clock (payload D2H / H2D included"
                    + (", and the HOST input's H2D" if loc == "host" else "") + "), median of 5"}
 
+    lanes = None
+    if args.lanes > 1 and loc == "device":
+        # several matrices in flight: `args.lanes` independent compress +
+        # decompress runtime pairs, each on its own stream, every lane a full
+        # round trip of its own copy of the matrix per step
+        L = B.lib()
+        # the single runtime's streams are released first: a process has few
+        # hardware queues, and each lane needs one of its own
+        B.compress_release()
+        B.decompress_release()
+        B.check(L.bsq_lanes_initialize(args.lanes, rows, cols, ro, rerr, svd, nit, uv, s, direct), "lanes init")
+        lsrc = [B.DeviceBuffer.from_array(x) for _ in range(args.lanes)]
+        ldst = [B.DeviceBuffer(x.nbytes) for _ in range(args.lanes)]
+
+        def lane_step():
+            for i in range(args.lanes):
+                B.check(L.bsq_lanes_roundtrip(i, lsrc[i].ptr, ldst[i].ptr), "lane round trip")
+
+        for _ in range(args.warmup):
+            lane_step()
+        B.check(L.bsq_lanes_synchronize(), "lanes sync")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            lane_step()
+        B.check(L.bsq_lanes_synchronize(), "lanes sync")
+        ldt = time.perf_counter() - t0
+        same = all(d.download(np.float32, n).tobytes() == out.tobytes() for d in ldst)
+        L.bsq_lanes_release()
+        del lsrc, ldst
+        if not same:
+            raise RuntimeError("a lane's decode differs from the single runtime's")
+        lanes = {"lanes": args.lanes, "ldt": ldt}
+        print(f"bench: {args.lanes} lanes, {ldt / args.steps * 1e3:.3f} ms per step", file=sys.stderr, flush=True)
+
     if args.calibrate_copy:
         # known-size copy for rocprofv3 --pmc calibration (FETCH_SIZE / WRITE_SIZE per byte)
+        stream = B.runtime_stream()  # the null stream once the lanes measurement released the runtimes
         for _ in range(3):
             B.check(B.lib().bsq_copy_kernel(dsrc.ptr, ddst.ptr, 4 * n, stream), "copy kernel")
         B.device_synchronize()
         print(f"bench: copy kernel calibration, {4 * n} bytes read + written per launch", file=sys.stderr)
 
+    # single-lane figures: one matrix at a time through the process-global
+    # runtimes (the reference ABI's model); with lanes, `value` and
+    # `ms_per_step` are those of the lanes measurement (L matrices per step)
+    single = {"value": round(value, 3), "unit": "GB/s", "ms_per_step": round(ms_per_step, 4),
+              "frac_of_roofline": round(t_roof / ms_per_step, 4),
+              "what": "one device-resident compress + decompress per step (bsq_device_compress / "
+                      "bsq_device_decompress on the process-global runtimes)"}
+    matrices = 1
+    if lanes:
+        matrices = lanes["lanes"]
+        ms_per_step = lanes["ldt"] / args.steps * 1e3
+        value = 4.0 * n * matrices * args.steps / lanes["ldt"] / 1e9
+        pipeline = {"t_roof_ms": round(t_roof, 4), "ms_per_matrix": round(ms_per_step / matrices, 4),
+                    "frac_of_roofline": round(t_roof * matrices / ms_per_step, 4)}
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
@@ -590,9 +648,11 @@ def main():
         "config": {"workload": args.workload, "rows": rows, "cols": cols, "outlier_topk_ratio": ro,
                    "error_correction_topk_ratio": rerr, "svd_ranks": svd, "svd_niters": nit,
                    "svd_uv_format": uv, "svd_s_format": s, "quantization_only_format": direct,
-                   "input": "device-resident", "rel_frobenius_error": round(rel, 6)},
+                   "input": "device-resident", "lanes": matrices, "matrices_per_step": matrices,
+                   "rel_frobenius_error": round(rel, 6)},
         "roofline": roofline,
         "pipeline_roofline": pipeline,
+        "single_lane": single,
         "abi_pcie_inclusive": abi,
     }
     if host_step:

@@ -101,6 +101,11 @@ def lib():
         "bsq_device_decompress": (i32, [C.POINTER(DevicePacked), P, u32]),
         "bsq_device_synchronize": (i32, []),
         "bsq_runtime_stream": (P, []),
+        "bsq_lanes_initialize": (i32, [i32, u16, u16, f32, f32, i32, i32, i32, i32, i32]),
+        "bsq_lanes_roundtrip": (i32, [i32, P, P]),
+        "bsq_lanes_stream": (P, [i32]),
+        "bsq_lanes_synchronize": (i32, []),
+        "bsq_lanes_release": (None, []),
         "bsq_topk_num_columns": (i32, [u16, f32, C.POINTER(u16)]),
         "bsq_topk_select": (i32, [P, u16, u16, u16, P, P, P, P]),
         "bsq_topk_scatter": (i32, [P, P, u16, u16, u16, P, i32, P]),

@@ -234,6 +234,8 @@ struct Runtime {
     bool reconstruct_initialized = false;
 
     hipStream_t stream = nullptr;
+    bool owns_stream = true;   // false: a lane's decompress runtime borrowing its compress stream
+    bool host_path = true;     // false: device-resident only (no copy stream, no pinned staging)
     hipEvent_t ev[8] = {};
     // payload copies between HBM and the pinned staging run on their own
     // stream (default priority), ordered after their producers by events, so
@@ -284,7 +286,7 @@ struct Runtime {
             if (e) (void)hipEventDestroy(e);
         if (t_begin) (void)hipEventDestroy(t_begin);
         if (t_end) (void)hipEventDestroy(t_end);
-        if (stream) (void)hipStreamDestroy(stream);
+        if (stream && owns_stream) (void)hipStreamDestroy(stream);
         if (copy_stream) (void)hipStreamDestroy(copy_stream);
         *this = Runtime{};
     }
@@ -383,9 +385,14 @@ void init_topk(TopkBuf &t, uint16_t rows, uint16_t cols, float ratio) {
     t.val = dev_alloc<float>(n);
 }
 
-void create_stream(Runtime &rt) {
-    BSQ_HIP(hipStreamCreateWithFlags(&rt.stream, hipStreamNonBlocking));
-    BSQ_HIP(hipStreamCreateWithFlags(&rt.copy_stream, hipStreamNonBlocking));
+void create_stream(Runtime &rt, hipStream_t borrowed = nullptr) {
+    if (borrowed) {
+        rt.stream = borrowed;
+        rt.owns_stream = false;
+    } else {
+        BSQ_HIP(hipStreamCreateWithFlags(&rt.stream, hipStreamNonBlocking));
+    }
+    if (rt.host_path) BSQ_HIP(hipStreamCreateWithFlags(&rt.copy_stream, hipStreamNonBlocking));
     for (auto &e : rt.ev) BSQ_HIP(hipEventCreate(&e));
     for (auto &e : rt.cev) BSQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     rt.meta = dev_alloc<Meta>(1);
@@ -423,9 +430,9 @@ void alloc_host_stage(Runtime &rt) {
 }
 
 // bitsqz_llm_compress_initialize body (src/bitsqz_llm.cu:785-885).
-void compress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int svd_ranks, int svd_niters,
-                   int uv, int s, int direct, int loc) {
-    Runtime &rt = g_comp;
+void compress_init(Runtime &rt, uint16_t rows, uint16_t cols, float r_out, float r_err, int svd_ranks,
+                   int svd_niters, int uv, int s, int direct, int loc, bool host_path = true) {
+    rt.host_path = host_path;
     rt.compress = true;
     rt.rows = rows;
     rt.cols = cols;
@@ -471,15 +478,15 @@ void compress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int s
     }
     BSQ_HIP(hipEventCreate(&rt.t_begin));
     BSQ_HIP(hipEventCreate(&rt.t_end));
-    alloc_host_stage(rt);
+    if (rt.host_path) alloc_host_stage(rt);
     BSQ_HIP(hipStreamSynchronize(rt.stream));
     rt.initialized = true;
 }
 
 // bitsqz_llm_decompress_initialize body (src/bitsqz_llm.cu:887-979).
-void decompress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int svd_ranks, int uv, int s,
-                     int direct) {
-    Runtime &rt = g_decomp;
+void decompress_init(Runtime &rt, uint16_t rows, uint16_t cols, float r_out, float r_err, int svd_ranks, int uv,
+                     int s, int direct, hipStream_t borrowed = nullptr) {
+    rt.host_path = borrowed == nullptr;
     rt.compress = false;
     rt.rows = rows;
     rt.cols = cols;
@@ -490,7 +497,7 @@ void decompress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int
     rt.uv_fmt = uv;
     rt.s_fmt = s;
     rt.direct_fmt = direct;
-    create_stream(rt);
+    create_stream(rt, borrowed);
     const uint64_t N = static_cast<uint64_t>(rows) * cols;
     if (svd_ranks >= 1) {
         rt.q = svd_ranks;
@@ -514,7 +521,7 @@ void decompress_init(uint16_t rows, uint16_t cols, float r_out, float r_err, int
     }
     if (r_out > 0.0f) init_topk(rt.topk[TK_OUTLIER], rows, cols, r_out);
     if (r_err > 0.0f) init_topk(rt.topk[TK_ERROR], rows, cols, r_err);
-    alloc_host_stage(rt);
+    if (rt.host_path) alloc_host_stage(rt);
     BSQ_HIP(hipStreamSynchronize(rt.stream));
     rt.initialized = true;
 }
@@ -1237,7 +1244,8 @@ int bitsqz_llm_compress_initialize(uint16_t num_rows, uint16_t num_columns, floa
     if (svd_niters < 1) return 1;
     bitsqz_llm_compress_release();
     const int rc = guarded([&] {
-        compress_init(num_rows, num_columns, outlier_topk_ratio, error_correction_topk_ratio, svd_ranks, svd_niters,
+        compress_init(g_comp, num_rows, num_columns, outlier_topk_ratio, error_correction_topk_ratio, svd_ranks,
+                      svd_niters,
                       svd_uv_format, svd_s_format, quantization_only_format, input_location);
     });
     if (rc != 0) {
@@ -1261,7 +1269,7 @@ int bitsqz_llm_decompress_initialize(uint16_t num_rows, uint16_t num_columns, fl
         return 1;
     bitsqz_llm_decompress_release();
     const int rc = guarded([&] {
-        decompress_init(num_rows, num_columns, outlier_topk_ratio, error_correction_topk_ratio, svd_ranks,
+        decompress_init(g_decomp, num_rows, num_columns, outlier_topk_ratio, error_correction_topk_ratio, svd_ranks,
                         svd_uv_format, svd_s_format, quantization_only_format);
     });
     if (rc != 0) {
@@ -1477,6 +1485,88 @@ int bsq_device_synchronize(void) {
 void *bsq_runtime_stream(void) {
     return g_comp.initialized ? static_cast<void *>(g_comp.stream) : static_cast<void *>(g_decomp.stream);
 }
+
+// ---------------------------------------------------------------------------
+// Lanes: independent compress + decompress runtime pairs, each on its own
+// non-blocking stream (default priority), for callers with several matrices
+// in flight.  A lane's round trip is the device-resident pipeline of
+// bsq_device_compress + bsq_device_decompress on its own buffers, so lanes
+// share nothing and need no ordering between them; the one-CU stages of one
+// lane's randomised SVD then run beside the other lanes' matrix-core GEMMs.
+// ---------------------------------------------------------------------------
+namespace {
+struct Lane {
+    Runtime comp, decomp;
+    bsq_device_packed_t last{};
+};
+std::vector<std::unique_ptr<Lane>> g_lanes;
+
+void lanes_release() noexcept {
+    for (auto &l : g_lanes) {
+        l->decomp.release();
+        l->comp.release();
+    }
+    g_lanes.clear();
+}
+}  // namespace
+
+int bsq_lanes_initialize(int lanes, uint16_t rows, uint16_t cols, float r_out, float r_err, int svd_ranks,
+                         int svd_niters, int uv, int s, int direct) {
+    lanes_release();
+    if (lanes < 1 || lanes > 8 || rows == 0 || cols == 0 || svd_niters < 1) {
+        set_error("bsq_lanes_initialize: 1 to 8 lanes, a non-empty shape and svd_niters >= 1");
+        return 1;
+    }
+    if (!ratio_is_valid(r_out) || !ratio_is_valid(r_err) || !method_is_valid(uv) || !method_is_valid(s) ||
+        !method_is_valid(direct)) {
+        set_error("bsq_lanes_initialize: invalid ratio or method");
+        return 1;
+    }
+    const int rc = guarded([&] {
+        const int q = svd_ranks >= 1 ? std::max(1, std::min(svd_ranks, static_cast<int>(std::min(rows, cols)))) : -1;
+        for (int i = 0; i < lanes; ++i) {
+            auto l = std::make_unique<Lane>();
+            // one stream per lane (a process has few hardware queues: with
+            // GPU_MAX_HW_QUEUES at its default of 4, extra streams share them
+            // and their work serialises), no copy stream, no host staging
+            compress_init(l->comp, rows, cols, r_out, r_err, svd_ranks, svd_niters, uv, s, direct,
+                          BITSQZ_LLM_INPUT_DEVICE, false);
+            decompress_init(l->decomp, rows, cols, r_out, r_err, q, uv, s, direct, l->comp.stream);
+            g_lanes.push_back(std::move(l));
+        }
+    });
+    if (rc != 0) {
+        const std::string msg = g_last_error;
+        lanes_release();
+        set_error(msg.c_str());
+    }
+    return rc;
+}
+
+int bsq_lanes_roundtrip(int lane, const float *d_input, float *d_dst) {
+    if (lane < 0 || lane >= static_cast<int>(g_lanes.size()) || !d_input || !d_dst) {
+        set_error("bsq_lanes_roundtrip: no such lane or null pointer");
+        return 1;
+    }
+    return guarded([&] {
+        Lane &l = *g_lanes[lane];
+        compress_device(l.comp, d_input, &l.last, false);
+        decompress_device(l.decomp, l.last, l.last.topk_k[1] > 0, d_dst, l.comp.stream, l.last.d_flags);
+    });
+}
+
+void *bsq_lanes_stream(int lane) {
+    if (lane < 0 || lane >= static_cast<int>(g_lanes.size())) return nullptr;
+    return g_lanes[lane]->comp.stream;
+}
+
+int bsq_lanes_synchronize(void) {
+    return guarded([&] {
+        for (auto &l : g_lanes) BSQ_HIP(hipStreamSynchronize(l->comp.stream));
+    });
+}
+
+void bsq_lanes_release(void) { lanes_release(); }
 
 int bsq_topk_num_columns(uint16_t num_columns, float ratio, uint16_t *out_k) {
     return guarded([&] {

@@ -133,6 +133,25 @@ BSQ_API int bsq_device_synchronize(void);
 /* The stream the runtimes enqueue on (a hipStream_t). */
 BSQ_API void *bsq_runtime_stream(void);
 
+/* Lanes (no counterpart in the reference, whose runtimes are process-global
+ * singletons, src/bitsqz_llm.cu:33-138): `lanes` (1..8) independent pairs of
+ * compress + decompress runtimes with the given configuration (DEVICE input;
+ * the decompress runtime takes the effective rank), each on its own stream.
+ * bsq_lanes_roundtrip enqueues one device-resident compress of d_input and
+ * the decompress of its result into d_dst (rows x cols floats) on the lane's
+ * stream, exactly as bsq_device_compress + bsq_device_decompress do, and
+ * returns without a host synchronisation.  Lanes share no buffers, so round
+ * trips on different lanes run concurrently; a lane's packed object lives
+ * until its next round trip.  For callers with several matrices in flight
+ * (e.g. the activations of several layers). */
+BSQ_API int bsq_lanes_initialize(int lanes, uint16_t rows, uint16_t cols, float outlier_topk_ratio,
+                                 float error_correction_topk_ratio, int svd_ranks, int svd_niters,
+                                 int svd_uv_format, int svd_s_format, int quantization_only_format);
+BSQ_API int bsq_lanes_roundtrip(int lane, const float *d_input, float *d_dst);
+BSQ_API void *bsq_lanes_stream(int lane);
+BSQ_API int bsq_lanes_synchronize(void);
+BSQ_API void bsq_lanes_release(void);
+
 /* ---------------------------------------------------------------------------
  * 3. Module operators
  * ------------------------------------------------------------------------- */
