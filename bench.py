@@ -13,7 +13,8 @@ stages of one matrix's randomised SVD run beside another's matrix-core GEMMs.
 the reference ABI's model).  Every lane's decode is checked byte for byte
 against the single-lane decode.  Prints one JSON line with the roofline
 figure of the dominant kernel and the reference's CPU codec timed on this
-host.  HOST-input workloads (c5) run single-lane.
+host.  For the HOST-input workload (c5) the lanes' figure is device-resident
+like the others, and `host_input_step` adds the H2D to a single-lane step.
 
 Dominant kernel: on the SVD workloads, the FP32-MFMA GEMMs that touch the
 full matrix (the range finder's 2 + 2 it products and the low-rank
@@ -586,7 +587,7 @@ def main():
                    + (", and the HOST input's H2D" if loc == "host" else "") + "), median of 5"}
 
     lanes = None
-    if args.lanes > 1 and loc == "device":
+    if args.lanes > 1:
         # several matrices in flight: `args.lanes` independent compress +
         # decompress runtime pairs, each on its own stream, every lane a full
         # round trip of its own copy of the matrix per step
