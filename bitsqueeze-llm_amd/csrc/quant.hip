@@ -99,13 +99,17 @@ __device__ __forceinline__ float group8_max(float v) {
     return v;
 }
 
-// Loads the 8 elements of `chunk` (zeros past n).
+// Loads the 8 elements of `chunk` (zeros past n).  The input is streamed:
+// non-temporal loads, which do not allocate in the caches (measured with the
+// caches holding other dirty data, as the pipeline leaves them: 53 us instead
+// of 77 us for the NF4 encode of 4096 x 11008, 93 instead of 125 us for the
+// two NF4_DQ passes).
 __device__ __forceinline__ void load8(const float *__restrict__ x, uint64_t n, uint64_t chunk,
                                       bool vec_ok, float (&v)[8]) {
     const uint64_t e0 = chunk * 8;
     if (vec_ok && e0 + 8 <= n) {
-        const float4 a = *reinterpret_cast<const float4 *>(x + e0);
-        const float4 b = *(reinterpret_cast<const float4 *>(x + e0) + 1);
+        const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(x + e0));
+        const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(x + e0) + 1);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
@@ -341,7 +345,10 @@ __global__ __launch_bounds__(kThreads) void quant_decode_kernel(
         float4 *o = reinterpret_cast<float4 *>(out + t * kDecTile);
         const float4 *src = reinterpret_cast<const float4 *>(tile[buf]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[threadIdx.x + kThreads * j] = src[threadIdx.x + kThreads * j];
+        for (int j = 0; j < 4; ++j) {  // non-temporal: the output is not read again here
+            const float4 v = src[threadIdx.x + kThreads * j];
+            __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4 *>(o + threadIdx.x + kThreads * j));
+        }
         // the next tile writes the other buffer; this one is reused two
         // tiles later, after the barrier of the next tile
     }

@@ -67,7 +67,8 @@ __device__ __forceinline__ float load_value(const TopkArgs &a, const float *Ls, 
 // scale, decoded exactly as load_value does element by element.
 template <TopkSource SRC>
 __device__ __forceinline__ void load_quad(const TopkArgs &a, const float *Ls, float dq, uint64_t e, float (&v)[4]) {
-    const float4 x = *reinterpret_cast<const float4 *>(a.a + e);
+    // a is streamed (read once here): a non-temporal load
+    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.a + e));
     if constexpr (SRC == TopkSource::Dense) {
         v[0] = x.x;
         v[1] = x.y;
@@ -546,7 +547,8 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         const uint32_t c4 = tid + kThreads * m;
         if (c4 < q4) {
             if constexpr (SRC == TopkSource::Dense) {
-                const float4 x = reinterpret_cast<const float4 *>(a.a + row0)[c4];
+                // streamed: a non-temporal load
+                const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.a + row0) + c4);
                 v[m][0] = x.x;
                 v[m][1] = x.y;
                 v[m][2] = x.z;
