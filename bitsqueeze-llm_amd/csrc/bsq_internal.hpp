@@ -87,6 +87,11 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
 // NF4_DQ encode whose global max of the block absmax is already known per row
 // (row_gmax[0 .. rows), from the outlier separation): one small reduce, then
 // the encode pass; the same bytes as launch_quant_encode.
+// NF4_DQ global scale input: *gmax = bits of the largest block absmax of x
+// (the first pass of launch_quant_encode; `codes` is scratch here, at least
+// ceil(n / 2) bytes), or, from per-row maxima, of row_gmax[0 .. rows).
+void launch_nf4dq_gmax(const float *x, uint64_t n, uint8_t *codes, uint32_t *gmax, hipStream_t stream);
+void launch_rows_gmax(const float *row_gmax, uint32_t rows, uint32_t *gmax, hipStream_t stream);
 void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gmax, uint32_t rows,
                                  uint8_t *scales_u8, float *dq_out, uint8_t *codes, uint32_t *gmax_scratch,
                                  hipStream_t stream);
@@ -119,6 +124,11 @@ enum class TopkSource : int {
     DenseMinusNF4 = 1,  // v = a[r, c] - dequant_nf4(...)[r, c]
     DenseMinusNF4DQ = 2,
     DenseMinusDense = 3,  // v = a[r, c] - b[r, c]
+    // a is first encoded (NF4 / NF4_DQ, written to enc_*), then
+    // v = a[r, c] - dequant(that encoding)[r, c]: the direct section's
+    // encode and its error pass in one read of a
+    EncodeNF4 = 4,
+    EncodeNF4DQ = 5,
 };
 struct TopkArgs {
     const float *a = nullptr;         // row-major rows x cols
@@ -140,7 +150,18 @@ struct TopkArgs {
     // written 0 by the kernel before anything else reads it (the compress
     // flags word: the separation clears it instead of a memset launch)
     uint32_t *flags_reset = nullptr;
+    // Encode sources: the section's codes (two per byte, element 2j in the
+    // high nibble), block scales, and for NF4_DQ the bits of the largest
+    // block absmax (input) and the raw global scale (written by row 0)
+    uint8_t *enc_codes = nullptr;
+    float *enc_scales_f32 = nullptr;
+    uint8_t *enc_scales_u8 = nullptr;
+    const uint32_t *enc_gmax = nullptr;
+    float *enc_dq_out = nullptr;
 };
+// True when the fused encode + top-k pass (TopkSource::EncodeNF4 / EncodeNF4DQ)
+// serves this shape: the register-resident kernel's shapes with cols % 64 == 0.
+bool topk_encode_supported(uint32_t rows, uint32_t cols, uint32_t k, const float *a, const uint8_t *codes);
 // Returns true when row_gmax was requested and written (the register-resident
 // kernel on a Dense source with cols % 64 == 0); otherwise row_gmax is left
 // alone and the caller computes the global scale itself.  flags_reset is

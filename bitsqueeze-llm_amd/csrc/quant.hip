@@ -16,6 +16,7 @@
 // This file is compiled with -ffp-contract=off: every multiply and subtract
 // below must round on its own, as in the reference.
 #include "bsq_internal.hpp"
+#include "nf4_codec.hpp"
 #include "scalar_codecs.hpp"
 
 #include <cfloat>
@@ -24,68 +25,6 @@ namespace bsq {
 namespace {
 
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ float sanitize(float x) { return __builtin_isfinite(x) ? x : 0.0f; }
-
-// The reference's linear scan: first index minimising |fl(v - L[i])|
-// (quantization_cuda.cu:43-58).  Used only where |v| >= 2 or v is not finite.
-__device__ __noinline__ uint32_t nf4_code_scan(float v) {
-    constexpr float L[16] = BSQ_NF4_LEVELS;
-    if (!__builtin_isfinite(v)) v = 0.0f;
-    uint32_t best = 0;
-    float best_err = fabsf(v - L[0]);
-#pragma unroll
-    for (int i = 1; i < 16; ++i) {
-        const float err = fabsf(v - L[i]);
-        if (err < best_err) {
-            best_err = err;
-            best = i;
-        }
-    }
-    return best;
-}
-
-// Nearest NF4 code with the reference's tie rule: for |v| < 2 the scan's
-// answer is the number of exact decision thresholds at or below v, found
-// here with one table lookup and one comparison.  [-1, 1] is
-// cut into 256 bins of width 1/128; bin b holds code_lo = #{T_i <= -1 + b/128}
-// and the threshold lying inside the bin, if any (no bin holds two: the
-// closest thresholds are 0.085 apart).  Every threshold is at least 2.3e-4
-// from a bin edge, while the bin index floor((v + 1) * 128) computed in FP32
-// is off by one only for v within 1.2e-7 of an edge, where the count is the
-// same on both sides; v in [1, 2) and (-2, -1] clamp to the end bins (codes
-// 15 and 0).  |v| >= 2 and non-finite v take the scan.  Exhaustively
-// checked against the scan over all 2^32 floats by the GPU test suite.
-struct Nf4Table {
-    uint2 ent[256];  // (bits of the threshold inside bin b, code_lo): one 8-byte read
-};
-
-__device__ __forceinline__ void nf4_table_build(Nf4Table &t) {
-    constexpr float T[15] = BSQ_NF4_THRESHOLDS;
-    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
-        const float e0 = -1.0f + static_cast<float>(b) / 128.0f, e1 = -1.0f + static_cast<float>(b + 1) / 128.0f;
-        uint32_t lo = 0;
-        float thr = __builtin_inff();
-#pragma unroll
-        for (int i = 0; i < 15; ++i) {
-            lo += (T[i] <= e0) ? 1u : 0u;
-            if (T[i] > e0 && T[i] < e1) thr = T[i];
-        }
-        t.ent[b] = uint2{__float_as_uint(thr), lo};
-    }
-}
-
-// the table path alone: |v| < 2
-__device__ __forceinline__ uint32_t nf4_code_small(const Nf4Table &t, float v) {
-    const int b = min(max(static_cast<int>((v + 1.0f) * 128.0f), 0), 255);
-    const uint2 e = t.ent[b];
-    return e.y + ((v >= __uint_as_float(e.x)) ? 1u : 0u);
-}
-
-__device__ __forceinline__ uint32_t nf4_code(const Nf4Table &t, float v) {
-    if (fabsf(v) < 2.0f) return nf4_code_small(t, v);
-    return nf4_code_scan(v);
-}
 
 // max over the aligned group of 8 lanes (quad xor-1, quad xor-2, half-row
 // mirror), all lanes of the group active.
@@ -134,17 +73,6 @@ __device__ __forceinline__ void store_codes(uint8_t *__restrict__ codes, uint64_
     }
 }
 
-__device__ __forceinline__ float dq_raw_from_gmax(uint32_t gbits) {
-    // store_dq_scale_kernel (quantization_cuda.cu:222-233)
-    const float g = __uint_as_float(gbits);
-    if (g == 0.0f || !__builtin_isfinite(g)) return 1.0f;
-    return g / kE4M3Max;
-}
-
-__device__ __forceinline__ float dq_effective(float dq) {
-    // nf4_dq_compress_kernel / nf4_dq_decompress_kernel (quantization_cuda.cu:246-249, 324-327)
-    return (dq == 0.0f || !__builtin_isfinite(dq)) ? 1.0f : dq;
-}
 
 // Encode side: one thread owns chunks of 8 consecutive elements (two 16-byte
 // loads, one 4-byte store of packed nibbles), so a 64-element block is an
@@ -524,6 +452,33 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
+void launch_nf4dq_gmax(const float *x, uint64_t n, uint8_t *codes, uint32_t *gmax, hipStream_t stream) {
+    BSQ_REQUIRE(n > 0 && x && codes && gmax, "NF4_DQ global scale: bad arguments");
+    const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
+    const unsigned grid = grid_for(ceil_div(n, 8));
+    // the workgroup maxima go to the start of the code buffer, which the
+    // encode overwrites afterwards (ceil(n / 2) bytes hold 4 bytes for each
+    // of the at most n / 2048 workgroups), and one workgroup reduces them: no
+    // allocation, and no device-scope atomics on one word (those serialise
+    // across the XCDs, which held this pass to one workgroup per CU and
+    // ~4 TB/s)
+    uint32_t *partial = reinterpret_cast<uint32_t *>(codes);
+    if ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0 && 4ull * grid <= ceil_div(n, 2)) {
+        dq_gmax_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, partial);
+        rows_gmax_kernel<<<1, kThreads, 0, stream>>>(reinterpret_cast<const float *>(partial), grid, gmax);
+    } else {  // a code buffer that cannot hold aligned words: one workgroup per CU, atomics
+        BSQ_HIP(hipMemsetAsync(gmax, 0, sizeof(uint32_t), stream));
+        dq_gmax_kernel<false><<<grid_for(ceil_div(n, 8), 1), kThreads, 0, stream>>>(x, n, vec_ok, gmax);
+    }
+    BSQ_HIP(hipGetLastError());
+}
+
+void launch_rows_gmax(const float *row_gmax, uint32_t rows, uint32_t *gmax, hipStream_t stream) {
+    BSQ_REQUIRE(row_gmax && rows > 0 && gmax, "NF4_DQ global scale: bad arguments");
+    rows_gmax_kernel<<<1, kThreads, 0, stream>>>(row_gmax, rows, gmax);
+    BSQ_HIP(hipGetLastError());
+}
+
 void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f32, uint8_t *scales_u8,
                          float *dq_out, uint8_t *codes, uint32_t *gmax_scratch, hipStream_t stream) {
     BSQ_REQUIRE(n > 0, "quant encode: empty input");
@@ -537,21 +492,7 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
                                                                   nullptr, codes);
     } else if (method == kMethodNF4DQ) {
         BSQ_REQUIRE(scales_u8 && codes && dq_out && gmax_scratch, "quant encode: null NF4_DQ output");
-        // the workgroup maxima go to the start of the code buffer, which the
-        // encode below overwrites (ceil(n / 2) bytes hold 4 bytes for each of
-        // the at most n / 2048 workgroups), and one workgroup reduces them:
-        // no allocation, and no device-scope atomics on one word (those
-        // serialise across the XCDs, which held this pass to one workgroup
-        // per CU and ~4 TB/s)
-        uint32_t *partial = reinterpret_cast<uint32_t *>(codes);
-        if ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0 && 4ull * grid <= ceil_div(n, 2)) {
-            dq_gmax_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, partial);
-            rows_gmax_kernel<<<1, kThreads, 0, stream>>>(reinterpret_cast<const float *>(partial), grid,
-                                                         gmax_scratch);
-        } else {  // a code buffer that cannot hold aligned words: one workgroup per CU, atomics
-            BSQ_HIP(hipMemsetAsync(gmax_scratch, 0, sizeof(uint32_t), stream));
-            dq_gmax_kernel<false><<<grid_for(ceil_div(n, 8), 1), kThreads, 0, stream>>>(x, n, vec_ok, gmax_scratch);
-        }
+        launch_nf4dq_gmax(x, n, codes, gmax_scratch, stream);
         quant_encode_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8, gmax_scratch,
                                                                  dq_out, codes);
     } else {

@@ -625,7 +625,39 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
     } else {
         Section &D = rt.sec[SEC_DIRECT];
         mark(2);
-        if (D.method != kMethodNone) {
+        const bool fused = D.method != kMethodNone && te.capacity > 0 &&
+                           topk_encode_supported(rows, cols, te.capacity, residual, D.codes);
+        if (fused) {
+            // the encode and the error pass in one read of the residual:
+            // codes and block scales, then the top-k of residual -
+            // dequant(codes) (src/bitsqz_llm.cu:1171-1227)
+            D.dense = nullptr;
+            const bool dq = D.method == kMethodNF4DQ;
+            timed_launch(kTimeDirectEncode, st, [&] {
+                if (dq) {
+                    if (have_row_gmax) launch_rows_gmax(rt.d_row_gmax, rows, &rt.meta->gmax, st);
+                    else launch_nf4dq_gmax(residual, N, D.codes, &rt.meta->gmax, st);
+                }
+                TopkArgs a;
+                a.a = residual;
+                a.rows = rows;
+                a.cols = cols;
+                a.k = te.capacity;
+                a.indices = te.idx;
+                a.values = te.val;
+                a.flags = &rt.meta->flags;
+                a.source = dq ? TopkSource::EncodeNF4DQ : TopkSource::EncodeNF4;
+                a.enc_codes = D.codes;
+                a.enc_scales_f32 = D.scales_f32;
+                a.enc_scales_u8 = D.scales_u8;
+                a.enc_gmax = &rt.meta->gmax;
+                a.enc_dq_out = &rt.meta->dq[SEC_DIRECT];
+                launch_topk_select(a, st);
+            });
+            mark(3);
+            mark(4);
+            mark(5);
+        } else if (D.method != kMethodNone) {
             D.dense = nullptr;
             timed_launch(kTimeDirectEncode, st, [&] {
                 if (have_row_gmax && D.method == kMethodNF4DQ)

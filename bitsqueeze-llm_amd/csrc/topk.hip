@@ -15,6 +15,8 @@
 // HBM once; `v` can be computed on the fly as a - b or as a - dequant(NF4)
 // so that the error-correction pass never materialises the error matrix.
 #include "bsq_internal.hpp"
+#include "nf4_codec.hpp"
+#include "scalar_codecs.hpp"
 #include "wave_ops.hpp"
 
 #include <algorithm>
@@ -30,14 +32,6 @@ __device__ __forceinline__ uint32_t order_key(float v) {
     // |v| as an ordered integer, NaN below +0 (build_sort_inputs_kernel maps
     // NaN to -inf, topk_cuda_utils.cuh:62-66).
     return __builtin_isnan(v) ? 0u : (__float_as_uint(fabsf(v)) + 1u);
-}
-
-__device__ __forceinline__ float e4m3_decode(uint32_t v) {
-    const uint32_t ef = (v >> 3) & 15u, mf = v & 7u;
-    float r;
-    if (ef == 0) r = (static_cast<float>(mf) / 8.0f) * 0.015625f;
-    else r = (1.0f + static_cast<float>(mf) / 8.0f) * __builtin_ldexpf(1.0f, static_cast<int>(ef) - 7);
-    return (v & 0x80u) ? -r : r;
 }
 
 template <TopkSource SRC>
@@ -512,7 +506,9 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
 // the fallback when the filter keeps more than kFastCap entries.
 template <TopkSource SRC, int NV4>
 __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
+    constexpr bool ENC = SRC == TopkSource::EncodeNF4 || SRC == TopkSource::EncodeNF4DQ;
     __shared__ Shared sh;
+    __shared__ Nf4Table etab[ENC ? 1 : 1];  // encode sources: the NF4 code table
     __shared__ __attribute__((aligned(16))) unsigned long long bk[kFastCap];
     __shared__ float bv[kFastCap];
     const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
@@ -533,6 +529,14 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         dq = *a.dq;
         if (dq == 0.0f || !__builtin_isfinite(dq)) dq = 1.0f;
     }
+    if constexpr (ENC) {
+        nf4_table_build(etab[0]);
+        if constexpr (SRC == TopkSource::EncodeNF4DQ) {
+            const float raw = dq_raw_from_gmax(*a.enc_gmax);
+            dq = dq_effective(raw);
+            if (r == 0 && tid == 0) *a.enc_dq_out = raw;
+        }
+    }
     __syncthreads();
 
     const bool quad_ok = (SRC != TopkSource::DenseMinusNF4 && SRC != TopkSource::DenseMinusNF4DQ) ||
@@ -546,7 +550,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     for (int m = 0; m < NV4; ++m) {
         const uint32_t c4 = tid + kThreads * m;
         if (c4 < q4) {
-            if constexpr (SRC == TopkSource::Dense) {
+            if constexpr (SRC == TopkSource::Dense || ENC) {
                 // streamed: a non-temporal load
                 const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.a + row0) + c4);
                 v[m][0] = x.x;
@@ -562,6 +566,53 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         } else {
 #pragma unroll
             for (int u = 0; u < 4; ++u) v[m][u] = __builtin_nanf("");
+        }
+    }
+    if constexpr (ENC) {
+        // Encode, exactly as quant_encode_kernel does chunk by chunk: the
+        // quads of the 16 lanes of one DPP row at one m are one 64-element
+        // block (cols % 64 == 0); block absmax of the sanitised values,
+        // scale (NF4: the absmax; NF4_DQ: dq * E4M3(absmax / dq)), codes of
+        // v / scale.  Then v becomes the error a - scale * L[code] of the
+        // raw value, as the DenseMinusNF4(DQ) sources compute it from the
+        // stored encoding.  Padding rows (whole DPP rows past the row end)
+        // store nothing and stay NaN.
+#pragma unroll
+        for (int m = 0; m < NV4; ++m) {
+            const uint32_t c4 = tid + kThreads * m;
+            const bool inside = c4 < q4;
+            float sv[4], lm = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                sv[u] = sanitize(v[m][u]);
+                lm = fmaxf(lm, fabsf(sv[u]));
+            }
+            const float bm = row16_max(lm);
+            const float absmax = (bm > 0.0f) ? bm : 1.0f;
+            float scale;
+            uint32_t scode = 0;
+            if constexpr (SRC == TopkSource::EncodeNF4DQ) {
+                scode = e4m3_encode(absmax / dq);
+                scale = dq * e4m3_decode(scode);
+                if (scale == 0.0f || !__builtin_isfinite(scale)) scale = 1.0f;
+            } else {
+                scale = absmax;
+            }
+            const float inv = 1.0f / scale;
+            uint32_t c[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) c[u] = nf4_code(etab[0], sv[u] * inv);
+            const uint64_t e = row0 + 4ull * c4;
+            if (inside) {
+                *reinterpret_cast<uint16_t *>(a.enc_codes + (e >> 1)) =
+                    static_cast<uint16_t>(((c[0] << 4) | c[1]) | (((c[2] << 4) | c[3]) << 8));
+                if ((tid & 15u) == 0) {
+                    if constexpr (SRC == TopkSource::EncodeNF4DQ) a.enc_scales_u8[e >> 6] = static_cast<uint8_t>(scode);
+                    else a.enc_scales_f32[e >> 6] = scale;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[m][u] = inside ? v[m][u] - scale * sh.L[c[u]] : __builtin_nanf("");
         }
     }
     // keys are recomputed from the values in every phase (an opaque copy of
@@ -1011,6 +1062,16 @@ void launch_src(const TopkArgs &a, hipStream_t stream) {
 
 }  // namespace
 
+bool topk_encode_supported(uint32_t rows, uint32_t cols, uint32_t k, const float *a, const uint8_t *codes) {
+    TopkArgs t;
+    t.a = a;
+    t.rows = rows;
+    t.cols = cols;
+    t.k = k;
+    return rows > 0 && rows <= 65535 && k >= 1 && cols % 64 == 0 && cols <= 65535 && reg_eligible(t) &&
+           (reinterpret_cast<uintptr_t>(codes) & 1u) == 0;
+}
+
 bool launch_topk_select(const TopkArgs &args, hipStream_t stream) {
     TopkArgs a = args;
     const bool reg = a.k >= 1 && a.k <= kTopkMaxK && reg_eligible(a);
@@ -1038,6 +1099,18 @@ bool launch_topk_select(const TopkArgs &args, hipStream_t stream) {
             BSQ_REQUIRE(a.scales_u8 && a.codes && a.dq, "top-k: null NF4_DQ subtrahend");
             launch_src<TopkSource::DenseMinusNF4DQ>(a, stream);
             break;
+        case TopkSource::EncodeNF4:
+        case TopkSource::EncodeNF4DQ: {
+            const bool dq = a.source == TopkSource::EncodeNF4DQ;
+            BSQ_REQUIRE(topk_encode_supported(a.rows, a.cols, a.k, a.a, a.enc_codes) && !a.residual,
+                        "top-k: shape outside the fused encode pass");
+            BSQ_REQUIRE(dq ? (a.enc_scales_u8 && a.enc_gmax && a.enc_dq_out) : (a.enc_scales_f32 != nullptr),
+                        "top-k: null encode output");
+            const bool ok = dq ? try_launch_reg<TopkSource::EncodeNF4DQ>(a, stream)
+                               : try_launch_reg<TopkSource::EncodeNF4>(a, stream);
+            BSQ_REQUIRE(ok, "top-k: fused encode pass not launched");
+            break;
+        }
     }
     BSQ_HIP(hipGetLastError());
     return gmax;

@@ -268,13 +268,13 @@ def test_device_resident_direct_decode_fused_with_the_scatter(rows, cols, fmt, r
 
 @pytest.mark.parametrize("fmt", [B.NF4, B.NF4_DQ])
 def test_direct_separation_keys_edge_rows(fmt):
-    """The quantised direct path with an outlier separation keeps only each
-    row's k-th largest composite key (no residual is written); the encode
-    and the error pass zero the selected entries of the input themselves.
-    Rows whose k-th entry is a NaN (fewer than k numbers: every number and the
-    lowest-column NaNs are separated), ties at the k-th magnitude (lower
-    columns win), infinities, all-zero and signed-zero rows give the oracle's
-    bytes and decode, through the ABI and the device-resident twin."""
+    """The quantised direct path with an outlier separation and an error
+    pass (cols % 64 == 0: the encode and the error top-k run as one fused
+    pass over the residual).  Rows whose k-th entry is a NaN (fewer than k
+    numbers: every number and the lowest-column NaNs are separated), ties at
+    the k-th magnitude (lower columns win), infinities, all-zero and
+    signed-zero rows give the oracle's bytes and decode, through the ABI and
+    the device-resident twin."""
     rows, cols = 24, 512
     rng = np.random.default_rng(11)
     x = rng.standard_normal((rows, cols)).astype(np.float32)
