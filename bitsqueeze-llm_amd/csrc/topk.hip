@@ -738,21 +738,37 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         total = k;
         exact = true;
     }
-    // collect the candidates with their values, then rank them
+    // collect the candidates with their values, then rank them (on the
+    // filter path the key is formed only for the few entries that pass)
     uint32_t pos = incl - cnt;
     lt = lane_id();
+    if (!exact) {  // uniform
 #pragma unroll
-    for (int m = 0; m < NV4; ++m) {
+        for (int m = 0; m < NV4; ++m) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const unsigned long long K = key_of(lt, m, u);
-            if (exact ? (K >= kt) : th.reaches_key(v[m][u])) {
-                bk[pos] = K;
-                bv[pos] = v[m][u];
-                ++pos;
+            for (int u = 0; u < 4; ++u) {
+                if (th.reaches_key(v[m][u])) {
+                    bk[pos] = key_of(lt, m, u);
+                    bv[pos] = v[m][u];
+                    ++pos;
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+        for (int m = 0; m < NV4; ++m) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const unsigned long long K = key_of(lt, m, u);
+                if (K >= kt) {
+                    bk[pos] = K;
+                    bv[pos] = v[m][u];
+                    ++pos;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     __syncthreads();
     uint16_t *out_idx = a.indices + static_cast<uint64_t>(r) * k;
