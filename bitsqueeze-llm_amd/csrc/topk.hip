@@ -508,7 +508,7 @@ template <TopkSource SRC, int NV4>
 __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     constexpr bool ENC = SRC == TopkSource::EncodeNF4 || SRC == TopkSource::EncodeNF4DQ;
     __shared__ Shared sh;
-    __shared__ Nf4Table etab[ENC ? 1 : 1];  // encode sources: the NF4 code table
+    __shared__ Nf4Table etab;  // encode sources: the NF4 code table (unused, and dropped, otherwise)
     __shared__ __attribute__((aligned(16))) unsigned long long bk[kFastCap];
     __shared__ float bv[kFastCap];
     const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         if (dq == 0.0f || !__builtin_isfinite(dq)) dq = 1.0f;
     }
     if constexpr (ENC) {
-        nf4_table_build(etab[0]);
+        nf4_table_build(etab);
         if constexpr (SRC == TopkSource::EncodeNF4DQ) {
             const float raw = dq_raw_from_gmax(*a.enc_gmax);
             dq = dq_effective(raw);
@@ -601,7 +601,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
             const float inv = 1.0f / scale;
             uint32_t c[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) c[u] = nf4_code(etab[0], sv[u] * inv);
+            for (int u = 0; u < 4; ++u) c[u] = nf4_code(etab, sv[u] * inv);
             const uint64_t e = row0 + 4ull * c4;
             if (inside) {
                 *reinterpret_cast<uint16_t *>(a.enc_codes + (e >> 1)) =
