@@ -373,9 +373,10 @@ __global__ __launch_bounds__(kRowThreads) void quant_decode_rows_kernel(
     }
     __syncthreads();
     if (vec_ok) {
-        float4 *o = reinterpret_cast<float4 *>(out + e0);
-        const float4 *src = reinterpret_cast<const float4 *>(row);
-        for (uint32_t i = t; i < cols / 4; i += kRowThreads) o[i] = src[i];
+        f32x4 *o = reinterpret_cast<f32x4 *>(out + e0);
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(row);
+        // non-temporal: the decoded matrix is not read again here
+        for (uint32_t i = t; i < cols / 4; i += kRowThreads) __builtin_nontemporal_store(src[i], o + i);
     } else {
         for (uint32_t i = t; i < cols; i += kRowThreads) out[e0 + i] = row[i];
     }
