@@ -80,10 +80,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // NF4 (method 11): scales_f32[ceil(n/64)], codes[ceil(n/2)].
 // NF4_DQ (method 10): scales_u8[ceil(n/64)], *dq_out, codes; `gmax_scratch`
-// is one device uint32 used for the global maximum.
+// is one device uint32 used for the global maximum.  A non-null `flags_reset`
+// (one device uint32) is set to 0 by the encode kernel.
 void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f32,
                          uint8_t *scales_u8, float *dq_out, uint8_t *codes,
-                         uint32_t *gmax_scratch, hipStream_t stream);
+                         uint32_t *gmax_scratch, hipStream_t stream, uint32_t *flags_reset = nullptr);
 // NF4_DQ encode whose global max of the block absmax is already known per row
 // (row_gmax[0 .. rows), from the outlier separation): one small reduce, then
 // the encode pass; the same bytes as launch_quant_encode.

@@ -133,8 +133,12 @@ template <bool DQ>
 __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     const float *__restrict__ x, uint64_t n, bool vec_ok, float *__restrict__ scales_f32,
     uint8_t *__restrict__ scales_u8, const uint32_t *__restrict__ gmax, float *__restrict__ dq_out,
-    uint8_t *__restrict__ codes) {
+    uint8_t *__restrict__ codes, uint32_t *__restrict__ flags_reset) {
     __shared__ Nf4Table tab;
+    // the pipeline's flags word, cleared here when no earlier kernel of the
+    // compress does it (saves a fill launch); nothing reads it before this
+    // kernel ends
+    if (flags_reset && blockIdx.x == 0 && threadIdx.x == 0) *flags_reset = 0u;
     const uint64_t nchunks = ceil_div(n, 8);
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
     float dq = 1.0f;  // NF4_DQ: set below, before the first encode
@@ -481,7 +485,8 @@ void launch_rows_gmax(const float *row_gmax, uint32_t rows, uint32_t *gmax, hipS
 }
 
 void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f32, uint8_t *scales_u8,
-                         float *dq_out, uint8_t *codes, uint32_t *gmax_scratch, hipStream_t stream) {
+                         float *dq_out, uint8_t *codes, uint32_t *gmax_scratch, hipStream_t stream,
+                         uint32_t *flags_reset) {
     BSQ_REQUIRE(n > 0, "quant encode: empty input");
     const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
     // one chunk per thread until the grid reaches its cap (small sections keep
@@ -490,12 +495,12 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
     if (method == kMethodNF4) {
         BSQ_REQUIRE(scales_f32 && codes, "quant encode: null NF4 output");
         quant_encode_kernel<false><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, scales_f32, nullptr, nullptr,
-                                                                  nullptr, codes);
+                                                                  nullptr, codes, flags_reset);
     } else if (method == kMethodNF4DQ) {
         BSQ_REQUIRE(scales_u8 && codes && dq_out && gmax_scratch, "quant encode: null NF4_DQ output");
         launch_nf4dq_gmax(x, n, codes, gmax_scratch, stream);
         quant_encode_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8, gmax_scratch,
-                                                                 dq_out, codes);
+                                                                 dq_out, codes, flags_reset);
     } else {
         fail("quant encode: unsupported method");
     }
@@ -512,7 +517,8 @@ void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gm
     rows_gmax_kernel<<<1, kThreads, 0, stream>>>(row_gmax, rows, gmax_scratch);
     BSQ_HIP(hipGetLastError());
     quant_encode_kernel<true><<<grid_for(ceil_div(n, 8)), kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8,
-                                                                                 gmax_scratch, dq_out, codes);
+                                                                                 gmax_scratch, dq_out, codes,
+                                                                                 nullptr);
     BSQ_HIP(hipGetLastError());
 }
 

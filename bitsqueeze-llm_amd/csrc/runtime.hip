@@ -576,9 +576,12 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
         timed_launch(kTimeTopkOutlier, st, [&] { have_row_gmax = launch_topk_select(a, st); });
         residual = rt.d_residual;
         flags |= kFlagOutlier;
-    } else {
-        BSQ_HIP(hipMemsetAsync(&rt.meta->flags, 0, sizeof(uint32_t), st));
     }
+    // without the separation the flags word is cleared by the direct quant
+    // encode when that is the only kernel before the readers, else by a fill
+    const Section &Dq = rt.sec[SEC_DIRECT];
+    const bool encode_clears = to.capacity == 0 && !has_svd && te.capacity == 0 && Dq.method != kMethodNone;
+    if (to.capacity == 0 && !encode_clears) BSQ_HIP(hipMemsetAsync(&rt.meta->flags, 0, sizeof(uint32_t), st));
     mark(1);
 
     if (has_svd) {
@@ -665,7 +668,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
                                                 &rt.meta->dq[SEC_DIRECT], D.codes, &rt.meta->gmax, st);
                 else
                     launch_quant_encode(residual, N, D.method, D.scales_f32, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
-                                        D.codes, &rt.meta->gmax, st);
+                                        D.codes, &rt.meta->gmax, st, encode_clears ? &rt.meta->flags : nullptr);
             });
             mark(3);
             mark(4);

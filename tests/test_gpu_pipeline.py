@@ -237,6 +237,33 @@ def test_device_resident_matches_abi(fmt, ro, re):
     B.decompress_release()
 
 
+def _device_flags(packed):
+    out = np.zeros(1, np.uint32)
+    B.check(B.lib().bsq_memcpy_d2h(out.ctypes.data_as(C.c_void_p), C.c_void_p(packed.d_flags), 4), "D2H")
+    return int(out[0])
+
+
+@pytest.mark.parametrize("fmt", [B.NF4, B.NF4_DQ])
+def test_device_flags_word_of_each_direct_variant(fmt):
+    """The device flags word of bsq_device_compress: bit 2 (error section
+    present) set after a compress with an error pass, and the word 0 after a
+    quant-only one (cleared by the encode kernel itself there, not by a fill)
+    even right after a compress that set it."""
+    rows, cols = 64, 4096
+    x = np.random.default_rng(9).standard_normal((rows, cols)).astype(np.float32)
+    for ro, re, want in [(0.0, 0.1, 4), (0.0, 0.0, 0), (0.02, 0.1, 4), (0.02, 0.0, 0), (0.0, 0.0, 0)]:
+        run_direct(x, ro, re, fmt)
+        src = B.DeviceBuffer.from_array(x)
+        for _ in range(2):
+            packed = B.device_compress(src)
+            B.device_synchronize()
+            word = _device_flags(packed)
+            assert (word & 4 if want else word) == want, (ro, re, word)
+        src.free()
+    B.compress_release()
+    B.decompress_release()
+
+
 @pytest.mark.parametrize("rows,cols,fmt,ro,re", [
     (37, 101, B.NF4, 0.03, 0.07),        # ragged width: element-wise decode of the fused row pass
     (33, 99, B.NF4_DQ, 0.02, 0.5),
