@@ -81,21 +81,25 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // NF4 (method 11): scales_f32[ceil(n/64)], codes[ceil(n/2)].
 // NF4_DQ (method 10): scales_u8[ceil(n/64)], *dq_out, codes; `gmax_scratch`
 // is one device uint32 used for the global maximum.  A non-null `flags_reset`
-// (one device uint32) is set to 0 by the encode kernel.
+// (one device uint32) is set to 0 by the encode kernel.  A non-null `sel`
+// (n % 64 == 0) is a selection bitmap over x (byte j, bit i = element
+// 8 j + i): flagged elements are encoded as 0 (x minus its separated
+// outliers, without a residual copy).
 void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f32,
                          uint8_t *scales_u8, float *dq_out, uint8_t *codes,
-                         uint32_t *gmax_scratch, hipStream_t stream, uint32_t *flags_reset = nullptr);
-// NF4_DQ encode whose global max of the block absmax is already known per row
-// (row_gmax[0 .. rows), from the outlier separation): one small reduce, then
-// the encode pass; the same bytes as launch_quant_encode.
+                         uint32_t *gmax_scratch, hipStream_t stream, uint32_t *flags_reset = nullptr,
+                         const uint8_t *sel = nullptr);
 // NF4_DQ global scale input: *gmax = bits of the largest block absmax of x
 // (the first pass of launch_quant_encode; `codes` is scratch here, at least
 // ceil(n / 2) bytes), or, from per-row maxima, of row_gmax[0 .. rows).
 void launch_nf4dq_gmax(const float *x, uint64_t n, uint8_t *codes, uint32_t *gmax, hipStream_t stream);
 void launch_rows_gmax(const float *row_gmax, uint32_t rows, uint32_t *gmax, hipStream_t stream);
+// NF4_DQ encode whose global max of the block absmax is already known per row
+// (row_gmax[0 .. rows), from the outlier separation): one small reduce, then
+// the encode pass; the same bytes as launch_quant_encode.
 void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gmax, uint32_t rows,
                                  uint8_t *scales_u8, float *dq_out, uint8_t *codes, uint32_t *gmax_scratch,
-                                 hipStream_t stream);
+                                 hipStream_t stream, const uint8_t *sel = nullptr);
 void launch_quant_decode(uint64_t n, int method, const float *scales_f32,
                          const uint8_t *scales_u8, const float *dq, const uint8_t *codes,
                          float *out, hipStream_t stream);
@@ -159,10 +163,25 @@ struct TopkArgs {
     uint8_t *enc_scales_u8 = nullptr;
     const uint32_t *enc_gmax = nullptr;
     float *enc_dq_out = nullptr;
+    // separation without a residual (Dense source, the register-resident
+    // kernel, cols % 64 == 0): bit (r * cols + c) of sel_bits (32-bit words,
+    // bit i of word w = element 32 w + i) is set when column c of row r is
+    // selected, i.e. zeroed in the residual a caller would otherwise read
+    uint32_t *sel_bits = nullptr;
+    // Encode sources: the input is `a` with the entries flagged in enc_sel
+    // (a sel_bits bitmap of the same shape) read as 0
+    const uint32_t *enc_sel = nullptr;
+    // Dense source: the input is read again right after this pass, so its
+    // loads allocate in the caches (otherwise they are non-temporal)
+    bool keep_input = false;
 };
 // True when the fused encode + top-k pass (TopkSource::EncodeNF4 / EncodeNF4DQ)
 // serves this shape: the register-resident kernel's shapes with cols % 64 == 0.
 bool topk_encode_supported(uint32_t rows, uint32_t cols, uint32_t k, const float *a, const uint8_t *codes);
+// True when the separation of k columns per row from `a` can write the
+// selection bitmap (TopkArgs::sel_bits) and the per-row block maxima instead
+// of a residual.
+bool topk_selbits_supported(uint32_t rows, uint32_t cols, uint32_t k, const float *a);
 // Returns true when row_gmax was requested and written (the register-resident
 // kernel on a Dense source with cols % 64 == 0); otherwise row_gmax is left
 // alone and the caller computes the global scale itself.  flags_reset is

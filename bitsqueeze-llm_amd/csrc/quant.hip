@@ -129,11 +129,14 @@ __global__ __launch_bounds__(kThreads) void dq_gmax_kernel(const float *__restri
     }
 }
 
-template <bool DQ>
+// SEL: sel[chunk] flags the chunk's elements that a separation took out
+// (bit i = element 8 chunk + i); they are encoded as 0, as the residual
+// holds them.
+template <bool DQ, bool SEL>
 __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     const float *__restrict__ x, uint64_t n, bool vec_ok, float *__restrict__ scales_f32,
     uint8_t *__restrict__ scales_u8, const uint32_t *__restrict__ gmax, float *__restrict__ dq_out,
-    uint8_t *__restrict__ codes, uint32_t *__restrict__ flags_reset) {
+    uint8_t *__restrict__ codes, uint32_t *__restrict__ flags_reset, const uint8_t *__restrict__ sel) {
     __shared__ Nf4Table tab;
     // the pipeline's flags word, cleared here when no earlier kernel of the
     // compress does it (saves a fill launch); nothing reads it before this
@@ -145,21 +148,29 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     // chunks of one iteration: loaded one iteration ahead (two register
     // sets), so the loads of iteration i + 1 are in flight while iteration i
     // is encoded
-    auto load_it = [&](uint64_t base, float (&v)[kUnroll][8]) {
+    auto load_it = [&](uint64_t base, float (&v)[kUnroll][8], uint32_t (&sb)[kUnroll]) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const uint64_t chunk = base + u * stride + threadIdx.x;
-            if (chunk < nchunks) load8(x, n, chunk, vec_ok, v[u]);
-            else
+            if (chunk < nchunks) {
+                load8(x, n, chunk, vec_ok, v[u]);
+                if constexpr (SEL) sb[u] = sel[chunk];
+            } else {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[u][i] = 0.0f;
+                if constexpr (SEL) sb[u] = 0u;
+            }
         }
     };
-    auto encode_it = [&](uint64_t base, float (&v)[kUnroll][8]) {
+    auto encode_it = [&](uint64_t base, float (&v)[kUnroll][8], const uint32_t (&sb)[kUnroll]) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const uint64_t chunk = base + u * stride + threadIdx.x;
             const bool valid = chunk < nchunks;
+            if constexpr (SEL) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[u][i] = ((sb[u] >> i) & 1u) ? 0.0f : v[u][i];
+            }
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[u][i] = sanitize(v[u][i]);
             float m = 0.0f;
@@ -207,12 +218,13 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     };
     const uint64_t step = static_cast<uint64_t>(kUnroll) * stride;
     float va[kUnroll][8], vb[kUnroll][8];
+    uint32_t sa[kUnroll] = {}, sbb[kUnroll] = {};
     uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads;
     // the first two iterations' loads go out before the code table is built
     // and the global scale read (neither feeds an address), so the table
     // work and the barrier overlap the first memory round trip
-    if (base < nchunks) load_it(base, va);
-    if (base + step < nchunks) load_it(base + step, vb);
+    if (base < nchunks) load_it(base, va, sa);
+    if (base + step < nchunks) load_it(base + step, vb, sbb);
     nf4_table_build(tab);
     if constexpr (DQ) {
         const float raw = dq_raw_from_gmax(*gmax);
@@ -221,11 +233,11 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     }
     __syncthreads();
     for (bool first = true; base < nchunks; base += 2 * step, first = false) {  // uniform
-        if (!first && base + step < nchunks) load_it(base + step, vb);
-        encode_it(base, va);
+        if (!first && base + step < nchunks) load_it(base + step, vb, sbb);
+        encode_it(base, va, sa);
         if (base + step >= nchunks) break;
-        if (base + 2 * step < nchunks) load_it(base + 2 * step, va);
-        encode_it(base + step, vb);
+        if (base + 2 * step < nchunks) load_it(base + 2 * step, va, sa);
+        encode_it(base + step, vb, sbb);
     }
 }
 
@@ -484,23 +496,38 @@ void launch_rows_gmax(const float *row_gmax, uint32_t rows, uint32_t *gmax, hipS
     BSQ_HIP(hipGetLastError());
 }
 
+namespace {
+// one chunk per thread until the grid reaches its cap (small sections keep
+// every CU busy); the unrolled loop then covers the rest
+template <bool DQ>
+void encode_pass(const float *x, uint64_t n, float *scales_f32, uint8_t *scales_u8, const uint32_t *gmax,
+                 float *dq_out, uint8_t *codes, uint32_t *flags_reset, const uint8_t *sel, hipStream_t stream) {
+    const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
+    const unsigned grid = grid_for(ceil_div(n, 8));
+    BSQ_REQUIRE(!sel || n % kQuantBlock == 0, "quant encode: a selection bitmap needs whole blocks");
+    if (sel)
+        quant_encode_kernel<DQ, true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, scales_f32, scales_u8, gmax,
+                                                                     dq_out, codes, flags_reset, sel);
+    else
+        quant_encode_kernel<DQ, false><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, scales_f32, scales_u8, gmax,
+                                                                      dq_out, codes, flags_reset, nullptr);
+    BSQ_HIP(hipGetLastError());
+}
+}  // namespace
+
 void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f32, uint8_t *scales_u8,
                          float *dq_out, uint8_t *codes, uint32_t *gmax_scratch, hipStream_t stream,
-                         uint32_t *flags_reset) {
+                         uint32_t *flags_reset, const uint8_t *sel) {
     BSQ_REQUIRE(n > 0, "quant encode: empty input");
-    const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
-    // one chunk per thread until the grid reaches its cap (small sections keep
-    // every CU busy); the unrolled loop then covers the rest
-    const unsigned grid = grid_for(ceil_div(n, 8));
     if (method == kMethodNF4) {
         BSQ_REQUIRE(scales_f32 && codes, "quant encode: null NF4 output");
-        quant_encode_kernel<false><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, scales_f32, nullptr, nullptr,
-                                                                  nullptr, codes, flags_reset);
+        encode_pass<false>(x, n, scales_f32, nullptr, nullptr, nullptr, codes, flags_reset, sel, stream);
     } else if (method == kMethodNF4DQ) {
         BSQ_REQUIRE(scales_u8 && codes && dq_out && gmax_scratch, "quant encode: null NF4_DQ output");
+        // the global scale pass reads x itself: the selected entries would count
+        BSQ_REQUIRE(!sel, "quant encode: NF4_DQ with a selection bitmap takes the per-row maxima");
         launch_nf4dq_gmax(x, n, codes, gmax_scratch, stream);
-        quant_encode_kernel<true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8, gmax_scratch,
-                                                                 dq_out, codes, flags_reset);
+        encode_pass<true>(x, n, nullptr, scales_u8, gmax_scratch, dq_out, codes, flags_reset, nullptr, stream);
     } else {
         fail("quant encode: unsupported method");
     }
@@ -510,16 +537,12 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
 
 void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gmax, uint32_t rows,
                                  uint8_t *scales_u8, float *dq_out, uint8_t *codes, uint32_t *gmax_scratch,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const uint8_t *sel) {
     BSQ_REQUIRE(n > 0 && rows > 0 && row_gmax && scales_u8 && codes && dq_out && gmax_scratch,
                 "quant encode: bad NF4_DQ arguments");
-    const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
     rows_gmax_kernel<<<1, kThreads, 0, stream>>>(row_gmax, rows, gmax_scratch);
     BSQ_HIP(hipGetLastError());
-    quant_encode_kernel<true><<<grid_for(ceil_div(n, 8)), kThreads, 0, stream>>>(x, n, vec_ok, nullptr, scales_u8,
-                                                                                 gmax_scratch, dq_out, codes,
-                                                                                 nullptr);
-    BSQ_HIP(hipGetLastError());
+    encode_pass<true>(x, n, nullptr, scales_u8, gmax_scratch, dq_out, codes, nullptr, sel, stream);
 }
 
 void launch_quant_decode(uint64_t n, int method, const float *scales_f32, const uint8_t *scales_u8,

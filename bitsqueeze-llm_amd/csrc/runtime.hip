@@ -560,6 +560,15 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
     TopkBuf &to = rt.topk[TK_OUTLIER];
     TopkBuf &te = rt.topk[TK_ERROR];
     const bool has_svd = rt.svd_ranks >= 1;
+    const Section &Dq = rt.sec[SEC_DIRECT];
+    // a quantised direct section after the separation: the separation writes
+    // a selection bitmap (one bit per element, in the residual buffer) and
+    // the encode reads the input with the flagged entries as 0, instead of
+    // writing the residual and reading it back
+    const bool selbits = !has_svd && to.capacity > 0 && Dq.method != kMethodNone &&
+                         topk_selbits_supported(rows, cols, to.capacity, d_in) &&
+                         (te.capacity == 0 || topk_encode_supported(rows, cols, te.capacity, d_in, Dq.codes));
+    uint32_t *sel = selbits ? reinterpret_cast<uint32_t *>(rt.d_residual) : nullptr;
     if (to.capacity > 0) {
         TopkArgs a;
         a.a = d_in;
@@ -568,18 +577,24 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
         a.k = to.capacity;
         a.indices = to.idx;
         a.values = to.val;
-        a.residual = rt.d_residual;
+        a.residual = selbits ? nullptr : rt.d_residual;
+        a.sel_bits = sel;
+        // the encode reads the input again right after: the separation's
+        // loads allocate in the caches (the 256 MB last-level cache serves
+        // part of the second read)
+        a.keep_input = selbits;
         // the direct NF4_DQ section's global scale needs the largest block
         // absmax of the residual: the separation kernel reports it per row
         a.row_gmax = rt.d_row_gmax;
         a.flags_reset = &rt.meta->flags;  // cleared here instead of a memset launch
         timed_launch(kTimeTopkOutlier, st, [&] { have_row_gmax = launch_topk_select(a, st); });
-        residual = rt.d_residual;
+        BSQ_REQUIRE(!selbits || have_row_gmax || Dq.method != kMethodNF4DQ,
+                    "compress: the bitmap separation reports the row maxima");
+        residual = selbits ? d_in : rt.d_residual;
         flags |= kFlagOutlier;
     }
     // without the separation the flags word is cleared by the direct quant
     // encode when that is the only kernel before the readers, else by a fill
-    const Section &Dq = rt.sec[SEC_DIRECT];
     const bool encode_clears = to.capacity == 0 && !has_svd && te.capacity == 0 && Dq.method != kMethodNone;
     if (to.capacity == 0 && !encode_clears) BSQ_HIP(hipMemsetAsync(&rt.meta->flags, 0, sizeof(uint32_t), st));
     mark(1);
@@ -631,9 +646,10 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
         const bool fused = D.method != kMethodNone && te.capacity > 0 &&
                            topk_encode_supported(rows, cols, te.capacity, residual, D.codes);
         if (fused) {
-            // the encode and the error pass in one read of the residual:
-            // codes and block scales, then the top-k of residual -
-            // dequant(codes) (src/bitsqz_llm.cu:1171-1227)
+            // the encode and the error pass in one read of the residual (or
+            // of the input and the separation's bitmap): codes and block
+            // scales, then the top-k of residual - dequant(codes)
+            // (src/bitsqz_llm.cu:1171-1227)
             D.dense = nullptr;
             const bool dq = D.method == kMethodNF4DQ;
             timed_launch(kTimeDirectEncode, st, [&] {
@@ -655,6 +671,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
                 a.enc_scales_u8 = D.scales_u8;
                 a.enc_gmax = &rt.meta->gmax;
                 a.enc_dq_out = &rt.meta->dq[SEC_DIRECT];
+                a.enc_sel = sel;
                 launch_topk_select(a, st);
             });
             mark(3);
@@ -663,12 +680,14 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
         } else if (D.method != kMethodNone) {
             D.dense = nullptr;
             timed_launch(kTimeDirectEncode, st, [&] {
+                const uint8_t *sel8 = reinterpret_cast<const uint8_t *>(sel);
                 if (have_row_gmax && D.method == kMethodNF4DQ)
                     launch_quant_encode_dq_rows(residual, N, rt.d_row_gmax, rows, D.scales_u8,
-                                                &rt.meta->dq[SEC_DIRECT], D.codes, &rt.meta->gmax, st);
+                                                &rt.meta->dq[SEC_DIRECT], D.codes, &rt.meta->gmax, st, sel8);
                 else
                     launch_quant_encode(residual, N, D.method, D.scales_f32, D.scales_u8, &rt.meta->dq[SEC_DIRECT],
-                                        D.codes, &rt.meta->gmax, st, encode_clears ? &rt.meta->flags : nullptr);
+                                        D.codes, &rt.meta->gmax, st, encode_clears ? &rt.meta->flags : nullptr,
+                                        sel8);
             });
             mark(3);
             mark(4);
@@ -676,6 +695,7 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
             if (te.capacity > 0) {
                 // error = residual - dequant(direct), computed inside the top-k
                 // kernel (src/bitsqz_llm.cu:1183-1227)
+                BSQ_REQUIRE(!selbits, "compress: the error pass reads a residual");
                 TopkArgs a;
                 a.a = residual;
                 a.rows = rows;

@@ -551,8 +551,10 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         const uint32_t c4 = tid + kThreads * m;
         if (c4 < q4) {
             if constexpr (SRC == TopkSource::Dense || ENC) {
-                // streamed: a non-temporal load
-                const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.a + row0) + c4);
+                // streamed: a non-temporal load, unless the caller reads the
+                // input again soon (keep_input: kept in the caches)
+                const f32x4 *src = reinterpret_cast<const f32x4 *>(a.a + row0) + c4;
+                const f32x4 x = (SRC == TopkSource::Dense && a.keep_input) ? *src : __builtin_nontemporal_load(src);
                 v[m][0] = x.x;
                 v[m][1] = x.y;
                 v[m][2] = x.z;
@@ -569,6 +571,18 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         }
     }
     if constexpr (ENC) {
+        if (a.enc_sel) {  // uniform: entries a separation took out read as 0
+            const uint32_t *srow = a.enc_sel + (row0 >> 5);
+#pragma unroll
+            for (int m = 0; m < NV4; ++m) {
+                const uint32_t c4 = tid + kThreads * m;
+                if (c4 < q4) {
+                    const uint32_t nib = srow[c4 >> 3] >> (4u * (c4 & 7u));
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) v[m][u] = ((nib >> u) & 1u) ? 0.0f : v[m][u];
+                }
+            }
+        }
         // Encode, exactly as quant_encode_kernel does chunk by chunk: the
         // quads of the 16 lanes of one DPP row at one m are one 64-element
         // block (cols % 64 == 0); block absmax of the sanitised values,
@@ -782,10 +796,10 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
             if (rank == k - 1) sh.kth = mine;
         }
     }
-    if (a.residual) {
+    if (a.residual || a.sel_bits) {  // uniform
         __syncthreads();
         const unsigned long long kth = sh.kth;
-        float4 *res4 = reinterpret_cast<float4 *>(a.residual + row0);
+        float4 *res4 = a.residual ? reinterpret_cast<float4 *>(a.residual + row0) : nullptr;
         lt = lane_id();
         const bool kth_number = (kth >> 16) != 0;  // uniform: the k-th largest is a number
         const MagThreshold mk(kth_number ? kth : (1ull << 16));
@@ -796,20 +810,23 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
 #pragma unroll
         for (int m = 0; m < NV4; ++m) {
             const uint32_t c4 = lt + kThreads * m;
+            bool s[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) s[u] = kth_number ? mk.reaches(v[m][u], 4 * c4 + u) : (key_of(lt, m, u) >= kth);
             float4 o;
-            if (kth_number) {
-                const uint32_t c = 4 * c4;
-                o.x = mk.reaches(v[m][0], c + 0) ? 0.0f : v[m][0];
-                o.y = mk.reaches(v[m][1], c + 1) ? 0.0f : v[m][1];
-                o.z = mk.reaches(v[m][2], c + 2) ? 0.0f : v[m][2];
-                o.w = mk.reaches(v[m][3], c + 3) ? 0.0f : v[m][3];
+            o.x = s[0] ? 0.0f : v[m][0];
+            o.y = s[1] ? 0.0f : v[m][1];
+            o.z = s[2] ? 0.0f : v[m][2];
+            o.w = s[3] ? 0.0f : v[m][3];
+            if (a.residual) {  // uniform
+                if (c4 < q4) res4[c4] = o;
             } else {
-                o.x = (key_of(lt, m, 0) >= kth) ? 0.0f : v[m][0];
-                o.y = (key_of(lt, m, 1) >= kth) ? 0.0f : v[m][1];
-                o.z = (key_of(lt, m, 2) >= kth) ? 0.0f : v[m][2];
-                o.w = (key_of(lt, m, 3) >= kth) ? 0.0f : v[m][3];
+                // the 8 lanes of an aligned group hold 32 consecutive columns
+                // (cols % 64 == 0): one bitmap word, its nibbles OR-ed together
+                const uint32_t nib = (s[0] ? 1u : 0u) | (s[1] ? 2u : 0u) | (s[2] ? 4u : 0u) | (s[3] ? 8u : 0u);
+                const uint32_t w = group8_or(nib << (4u * (c4 & 7u)));
+                if ((c4 & 7u) == 0 && c4 < q4) a.sel_bits[(row0 >> 5) + (c4 >> 3)] = w;
             }
-            if (c4 < q4) res4[c4] = o;
             if (a.row_gmax) {  // uniform
                 auto san = [](float x) { return __builtin_isfinite(x) ? fabsf(x) : 0.0f; };
                 const float bm = row16_max(fmaxf(fmaxf(san(o.x), san(o.y)), fmaxf(san(o.z), san(o.w))));
@@ -1088,11 +1105,25 @@ bool topk_encode_supported(uint32_t rows, uint32_t cols, uint32_t k, const float
            (reinterpret_cast<uintptr_t>(codes) & 1u) == 0;
 }
 
+bool topk_selbits_supported(uint32_t rows, uint32_t cols, uint32_t k, const float *a) {
+    TopkArgs t;
+    t.a = a;
+    t.rows = rows;
+    t.cols = cols;
+    t.k = k;
+    return rows > 0 && rows <= 65535 && k >= 1 && k <= kTopkMaxK && cols % 64 == 0 && cols <= 65535 &&
+           reg_eligible(t);
+}
+
 bool launch_topk_select(const TopkArgs &args, hipStream_t stream) {
     TopkArgs a = args;
     const bool reg = a.k >= 1 && a.k <= kTopkMaxK && reg_eligible(a);
-    const bool gmax = a.row_gmax && a.residual && a.source == TopkSource::Dense && a.cols % 64 == 0 && reg;
+    const bool gmax =
+        a.row_gmax && (a.residual || a.sel_bits) && a.source == TopkSource::Dense && a.cols % 64 == 0 && reg;
     if (!gmax) a.row_gmax = nullptr;
+    BSQ_REQUIRE(!a.sel_bits || (topk_selbits_supported(a.rows, a.cols, a.k, a.a) && !a.residual &&
+                                a.source == TopkSource::Dense),
+                "top-k: the selection bitmap needs a dense source in the register kernel's shapes");
     BSQ_REQUIRE(a.rows > 0 && a.cols > 0 && a.cols <= 65535 && a.rows <= 65535, "top-k: bad shape");
     BSQ_REQUIRE(a.k >= 1 && a.k <= a.cols, "top-k: k must be in [1, cols]");
     BSQ_REQUIRE(a.a && a.indices && a.values, "top-k: null pointer");

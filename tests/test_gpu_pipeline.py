@@ -270,6 +270,8 @@ def test_device_flags_word_of_each_direct_variant(fmt):
     (16, 4096, B.NF4, 0.15, 0.2),        # k = 614 and 819 per row: entries past the first 512
     (8, 4096, B.NF4, 0.0, 0.3),          # error set only
     (24, 4096, B.NF4_DQ, 0.05, 0.0),     # outlier set only
+    (32, 4096, B.NF4, 0.05, 0.0),        # outlier set only, NF4: the encode reads the input and the selection bitmap
+    (12, 2048, B.NF4, 0.2, 0.1),         # k_o = 409 per row: the separation writes a residual (LDS kernel)
     (64, 11008, B.NF4_DQ, 0.005, 0.01),  # the headline width
 ])
 def test_device_resident_direct_decode_fused_with_the_scatter(rows, cols, fmt, ro, re):
