@@ -436,6 +436,103 @@ __global__ __launch_bounds__(kBig) void sytrd_kernel(double *__restrict__ W, int
     }
 }
 
+// ---------------------------------------------------------------------------
+// Householder tridiagonalisation for 256 < k <= 512, the same reduction
+// (LAPACK dsytd2 order: reflector j from column j, p = A v, w = tau p -
+// (tau^2 / 2)(p.v) v, A -= v w^T + w v^T) spread over two kernels per column
+// on a global-memory working copy A (full symmetric storage):
+//   trd_col_kernel (one workgroup): w_{j-1} from p_{j-1}; row j of A with
+//     update j-1 applied (its column by symmetry); d[j]; reflector j (e[j],
+//     tau[j], v_j, and row j of H, zero up to column j);
+//   trd_update_kernel (one wave per row of the trailing block, many CUs):
+//     applies update j-1 to rows and columns > j and forms p_j = A v_j in
+//     the same pass.
+// Every column thus costs one read and one write of the trailing block on
+// all CUs instead of two reads and a write on one.  The last call (j = k-2)
+// only finishes w_{k-3}, d[k-2], e[k-2] and d[k-1].
+// ---------------------------------------------------------------------------
+constexpr int kTrdColThreads = 512;  // one index per lane (k <= 512)
+constexpr int kTrdRowsPerBlock = 4;  // one wave per row
+
+__global__ __launch_bounds__(kTrdColThreads) void trd_col_kernel(
+    const double *__restrict__ A, int k, int j, const double *__restrict__ vprev, const double *__restrict__ p,
+    double *__restrict__ w, double *__restrict__ vcur, double *__restrict__ d, double *__restrict__ e,
+    double *__restrict__ tau, double *__restrict__ H) {
+    __shared__ double red[kTrdColThreads / 64];
+    __shared__ double s_wj, s_alpha;
+    const int i = threadIdx.x;
+    const bool in = i < k;
+    // w_{j-1} on indices >= j (zero below): p_{j-1} = A_{j-1} v_{j-1}
+    double wi = 0.0, vpi = 0.0;
+    if (j > 0) {
+        const double tp = tau[j - 1];
+        const double pi = (in && i >= j) ? p[i] : 0.0;
+        vpi = (in && i >= j) ? vprev[i] : 0.0;
+        const double pv = block_sum(pi * vpi, red);
+        wi = tp * pi - (0.5 * tp * tp * pv) * vpi;
+        if (in) w[i] = wi;
+        if (i == j) s_wj = wi;
+        __syncthreads();
+    }
+    // row j with update j-1 applied (v_{j-1}[j] = 1), as trd_update_kernel
+    // would form it
+    double x = 0.0;
+    if (in && i >= j) {
+        x = A[static_cast<uint64_t>(j) * k + i];
+        if (j > 0) x -= (vprev[j] * wi + s_wj * vpi);
+    }
+    if (i == j) d[j] = x;
+    if (i == j + 1) s_alpha = x;
+    const double sig = block_sum((in && i >= j + 2) ? x * x : 0.0, red);
+    const double alpha = s_alpha;  // written before block_sum's barriers
+    double t = 0.0, beta = alpha, scal = 0.0;
+    if (sig > 0.0) {
+        const double nrm = sqrt(fma(alpha, alpha, sig));
+        beta = (alpha >= 0.0) ? -nrm : nrm;
+        t = (beta - alpha) / beta;
+        scal = 1.0 / (alpha - beta);
+    }
+    if (in) {
+        const double v = (i == j + 1) ? 1.0 : ((i > j + 1) ? x * scal : 0.0);
+        vcur[i] = v;
+        H[static_cast<uint64_t>(j) * k + i] = v;
+    }
+    if (i == 0) {
+        e[j] = beta;
+        tau[j] = t;
+    }
+    if (j == k - 2) {  // the last call: d[k-1] with update k-3, H's last row zero
+        if (i == k - 1) {
+            d[k - 1] = A[static_cast<uint64_t>(k - 1) * k + (k - 1)] - (vpi * wi + wi * vpi);
+            tau[k - 1] = 0.0;
+        }
+        if (in) H[static_cast<uint64_t>(k - 1) * k + i] = 0.0;
+    }
+}
+
+__global__ __launch_bounds__(256) void trd_update_kernel(double *__restrict__ A, int k, int j,
+                                                         const double *__restrict__ vprev,
+                                                         const double *__restrict__ w,
+                                                         const double *__restrict__ vcur, double *__restrict__ p) {
+    const int lane = threadIdx.x & 63;
+    const int r = j + 1 + static_cast<int>(blockIdx.x) * kTrdRowsPerBlock + static_cast<int>(threadIdx.x >> 6);
+    if (r >= k) return;  // whole waves
+    const bool upd = j > 0;
+    const double vr = upd ? vprev[r] : 0.0, wr = upd ? w[r] : 0.0;
+    double *row = A + static_cast<uint64_t>(r) * k;
+    double acc = 0.0;
+    for (int c = j + 1 + lane; c < k; c += 64) {
+        double a = row[c];
+        if (upd) {
+            a -= (vr * w[c] + wr * vprev[c]);
+            row[c] = a;
+        }
+        acc = fma(a, vcur[c], acc);
+    }
+    acc = wave_sum_dpp(acc);
+    if (lane == 0) p[r] = acc;
+}
+
 // Number of eigenvalues of the tridiagonal (d, e) strictly below x.
 __device__ int sturm_count(const double *d, const double *e2, int k, double x, double pivmin) {
     int cnt = 0;
@@ -991,15 +1088,17 @@ __global__ __launch_bounds__(kMsThreads) void multisect_kernel(const double *__r
 }
 
 // Back-transformation with row-wise reflectors H[j][*]: u_t = H_0 ... H_{k-3} z_t.
-// One wave per eigenvector with z in registers (KPL = ceil(k / 64) values
-// per lane); reflector rows are staged through LDS 32 at a time and shared
+// One wave per eigenvector with z in registers (KPL >= ceil(k / 64) values
+// per lane); reflector rows are staged through LDS RB at a time and shared
 // by the 4 waves of the workgroup; the dot products reduce through DPP.
-template <int KPL>
+template <int KPL, int RB = 32>
 __global__ __launch_bounds__(256) void backtransform_rows_kernel(const double *__restrict__ H,
                                                                  const double *__restrict__ tau, int k,
                                                                  const double *__restrict__ Z,
                                                                  float *__restrict__ Uh) {
-    constexpr int RB = 32, NQ = RB * KPL * 64 / 256;  // rows per stage, staged doubles per lane
+    // RB reflector rows per stage (two stages of RB * KPL * 64 doubles in LDS)
+    static_assert(RB % 2 == 0 && (RB * KPL * 64) % 256 == 0, "stage shape");
+    constexpr int NQ = RB * KPL * 64 / 256;  // staged doubles per lane
     __shared__ double hs[2][RB][KPL * 64];
     __shared__ double ts[2][RB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1152,9 +1251,25 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
     // below leave alone (they use 5k^2 + 4k^2 of its 9k^2 + 2k doubles)
     double *ext = scratch + 9ull * k * k;
     const size_t kb = static_cast<size_t>(k) * sizeof(double);
+    // reflectors row-wise in W (H[j][i]) from the register kernel (k <= 256)
+    // and the per-column kernels (k <= 512), column-wise otherwise
     bool reg = true;
     if (sytrd_blocked_supported(k)) {
         launch_sytrd_blocked(G, k, d, e, tau, W, stream);
+    } else if (k > 256 && k <= kTrdColThreads) {
+        // working copy and vectors in the scratch, which the eigenvector
+        // kernels below only use afterwards
+        double *A = scratch, *vb0 = scratch + static_cast<size_t>(k) * k, *vb1 = vb0 + k, *w = vb1 + k, *p = w + k;
+        BSQ_HIP(hipMemcpyAsync(A, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));
+        for (int j = 0; j + 2 <= k; ++j) {
+            double *vprev = (j & 1) ? vb0 : vb1, *vcur = (j & 1) ? vb1 : vb0;
+            trd_col_kernel<<<1, kTrdColThreads, 0, stream>>>(A, k, j, vprev, p, w, vcur, d, e, tau, W);
+            if (j + 3 <= k) {
+                const unsigned rows = static_cast<unsigned>(k - j - 1);
+                trd_update_kernel<<<static_cast<unsigned>(ceil_div(rows, kTrdRowsPerBlock)), 256, 0, stream>>>(
+                    A, k, j, vprev, w, vcur, p);
+            }
+        }
     } else {
         reg = false;
         BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));
@@ -1206,7 +1321,8 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
         if (k <= 64) backtransform_rows_kernel<1><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
         else if (k <= 128) backtransform_rows_kernel<2><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
         else if (k <= 192) backtransform_rows_kernel<3><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
-        else backtransform_rows_kernel<4><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
+        else if (k <= 256) backtransform_rows_kernel<4><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
+        else backtransform_rows_kernel<8, 16><<<g, 256, 0, stream>>>(W, tau, k, Z, Uh);
     } else
         backtransform_kernel<<<static_cast<unsigned>(ceil_div(k, 4)), 256, 0, stream>>>(W, tau, k, Z, Uh);
     BSQ_HIP(hipGetLastError());

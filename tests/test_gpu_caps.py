@@ -69,9 +69,10 @@ def test_svd_ranks_above_4096_small_rows_accepted():
 
 @pytest.mark.timeout(600)
 def test_svd_effective_rank_above_4096_matches_oracle():
-    """k = 4100 (both dimensions above 4096): the global-memory Cholesky,
-    tridiagonalisation and eigensolver kernels at a rank the round-one build
-    rejected."""
+    """k = 4100 (both dimensions above 4096): the unblocked global-memory
+    Cholesky, the one-workgroup tridiagonalisation (sytrd_kernel), the
+    column-wise back-transformation and the eigensolver kernels with their
+    global-memory vectors."""
     m, n, q = 4160, 4300, 4100
     A = lowrank(m, n, min(m, n), 0.5, 0.0, seed=9)
     R = np.random.default_rng(3).standard_normal((m, q)).astype(np.float32)

@@ -46,9 +46,10 @@ def svd_parity(A, q, it, R, tol_rec=1e-4, tol_s=1e-5):
     (2048, 14336, 512, 3, 0.8),  # C5's rank and iterations on its 8-way row share
 ])
 def test_svd_rank_above_256_matches_oracle(m, n, q, it, decay):
-    """Ranks above 256 run the global-memory Cholesky, tridiagonalisation and
-    back-transformation (linalg.hip chol_inv_kernel, sytrd_kernel,
-    backtransform_kernel) and the A B^T orthonormalisation products."""
+    """Ranks 257 .. 512 run the two-level Cholesky, the per-column
+    tridiagonalisation over a global-memory working copy (linalg.hip
+    trd_col_kernel + trd_update_kernel, reflectors row-wise) and the row-wise
+    back-transformation (backtransform_rows_kernel<8, 16>)."""
     A = lowrank(m, n, min(1024, m, n), decay, 0.02, seed=q)
     k = max(1, min(q, m, n))
     R = np.random.default_rng(3).standard_normal((min(m, n), k)).astype(np.float32)
