@@ -441,18 +441,18 @@ __global__ __launch_bounds__(kBig) void sytrd_kernel(double *__restrict__ W, int
 // (LAPACK dsytd2 order: reflector j from column j, p = A v, w = tau p -
 // (tau^2 / 2)(p.v) v, A -= v w^T + w v^T) spread over two kernels per column
 // on a global-memory working copy A (full symmetric storage):
-//   trd_col_kernel (one workgroup): w_{j-1} from p_{j-1}; row j of A with
-//     update j-1 applied (its column by symmetry); d[j]; reflector j (e[j],
-//     tau[j], v_j, and row j of H, zero up to column j);
-//   trd_update_kernel (one wave per row of the trailing block, many CUs):
-//     applies update j-1 to rows and columns > j and forms p_j = A v_j in
-//     the same pass.
-// Every column thus costs one read and one write of the trailing block on
-// all CUs instead of two reads and a write on one.  The last call (j = k-2)
-// only finishes w_{k-3}, d[k-2], e[k-2] and d[k-1].
+//   trd_step_kernel (one launch per column, many CUs): every workgroup
+//     forms w_{j-1} from p_{j-1}, row j of A with update j-1 applied (its
+//     column by symmetry) and reflector j; workgroup 0 writes d[j], e[j],
+//     tau[j] and row j of H (zero up to column j); then one wave per row of
+//     the trailing block applies update j-1 and forms p_j = A v_j in the
+//     same pass;
+//   trd_col_kernel (one workgroup) finishes the last column: w_{k-3},
+//     d[k-2], e[k-2] and d[k-1].
+// Every column thus costs one launch and one read and write of the
+// trailing block on all CUs, instead of two reads and a write on one CU.
 // ---------------------------------------------------------------------------
 constexpr int kTrdColThreads = 512;  // one index per lane (k <= 512)
-constexpr int kTrdRowsPerBlock = 4;  // one wave per row
 
 __global__ __launch_bounds__(kTrdColThreads) void trd_col_kernel(
     const double *__restrict__ A, int k, int j, const double *__restrict__ vprev, const double *__restrict__ p,
@@ -474,8 +474,8 @@ __global__ __launch_bounds__(kTrdColThreads) void trd_col_kernel(
         if (i == j) s_wj = wi;
         __syncthreads();
     }
-    // row j with update j-1 applied (v_{j-1}[j] = 1), as trd_update_kernel
-    // would form it
+    // row j with update j-1 applied (v_{j-1}[j] = 1), as trd_step_kernel
+    // forms it
     double x = 0.0;
     if (in && i >= j) {
         x = A[static_cast<uint64_t>(j) * k + i];
@@ -510,27 +510,90 @@ __global__ __launch_bounds__(kTrdColThreads) void trd_col_kernel(
     }
 }
 
-__global__ __launch_bounds__(256) void trd_update_kernel(double *__restrict__ A, int k, int j,
-                                                         const double *__restrict__ vprev,
-                                                         const double *__restrict__ w,
-                                                         const double *__restrict__ vcur, double *__restrict__ p) {
-    const int lane = threadIdx.x & 63;
-    const int r = j + 1 + static_cast<int>(blockIdx.x) * kTrdRowsPerBlock + static_cast<int>(threadIdx.x >> 6);
-    if (r >= k) return;  // whole waves
-    const bool upd = j > 0;
-    const double vr = upd ? vprev[r] : 0.0, wr = upd ? w[r] : 0.0;
-    double *row = A + static_cast<uint64_t>(r) * k;
-    double acc = 0.0;
-    for (int c = j + 1 + lane; c < k; c += 64) {
-        double a = row[c];
-        if (upd) {
-            a -= (vr * w[c] + wr * vprev[c]);
-            row[c] = a;
+// One column step j = 0 .. k-3 in one launch: every workgroup forms w_{j-1}
+// and reflector j itself from the same data in the same order (so they all
+// hold the same bits; workgroup 0 writes d[j], e[j], tau[j] and row j of H),
+// then its waves take one trailing row each: update j-1 applied, p_j = A v_j.
+// p is double-buffered: this launch reads p_{j-1} in every workgroup while
+// others already write p_j.
+constexpr int kTrdStepThreads = 512;  // one index per lane (k <= 512), 8 rows per workgroup
+__global__ __launch_bounds__(kTrdStepThreads) void trd_step_kernel(
+    double *__restrict__ A, int k, int j, const double *__restrict__ pprev, double *__restrict__ pout,
+    double *__restrict__ d, double *__restrict__ e, double *__restrict__ tau, double *__restrict__ H) {
+    __shared__ double red[kTrdStepThreads / 64];
+    __shared__ double s_wj, s_alpha;
+    __shared__ double sw[kTrdStepThreads], svp[kTrdStepThreads], sv[kTrdStepThreads];
+    const int i = threadIdx.x;
+    const bool in = i < k;
+    const bool lead = blockIdx.x == 0;
+    // w_{j-1} on indices >= j (zero below); v_{j-1} is row j-1 of H
+    double wi = 0.0, vpi = 0.0;
+    if (j > 0) {
+        const double tp = tau[j - 1];
+        const double pi = (in && i >= j) ? pprev[i] : 0.0;
+        vpi = (in && i >= j) ? H[static_cast<uint64_t>(j - 1) * k + i] : 0.0;
+        const double pv = block_sum(pi * vpi, red);
+        wi = tp * pi - (0.5 * tp * tp * pv) * vpi;
+        if (i == j) s_wj = wi;
+        __syncthreads();
+    }
+    sw[i] = wi;
+    svp[i] = vpi;
+    // row j with update j-1 applied (v_{j-1}[j] = 1)
+    double x = 0.0;
+    if (in && i >= j) {
+        x = A[static_cast<uint64_t>(j) * k + i];
+        if (j > 0) x -= (H[static_cast<uint64_t>(j - 1) * k + j] * wi + s_wj * vpi);
+    }
+    if (lead && i == j) d[j] = x;
+    if (i == j + 1) s_alpha = x;
+    const double sig = block_sum((in && i >= j + 2) ? x * x : 0.0, red);
+    const double alpha = s_alpha;
+    double t = 0.0, beta = alpha, scal = 0.0;
+    if (sig > 0.0) {
+        const double nrm = sqrt(fma(alpha, alpha, sig));
+        beta = (alpha >= 0.0) ? -nrm : nrm;
+        t = (beta - alpha) / beta;
+        scal = 1.0 / (alpha - beta);
+    }
+    const double v = (in && i == j + 1) ? 1.0 : ((in && i > j + 1) ? x * scal : 0.0);
+    sv[i] = v;
+    if (lead) {
+        if (in) H[static_cast<uint64_t>(j) * k + i] = v;
+        if (i == 0) {
+            e[j] = beta;
+            tau[j] = t;
         }
-        acc = fma(a, vcur[c], acc);
+    }
+    __syncthreads();
+    // trailing rows: update j-1, then p_j = A v_j
+    const int lane = i & 63;
+    const int r = j + 1 + static_cast<int>(blockIdx.x) * (kTrdStepThreads / 64) + (i >> 6);
+    if (r >= k) return;  // whole waves, after the last barrier
+    const bool upd = j > 0;
+    const double vr = svp[r], wr = sw[r];
+    double *row = A + static_cast<uint64_t>(r) * k;
+    constexpr int kMaxIt = kTrdStepThreads / 64;  // k <= 512: at most 8 columns per lane
+    double a[kMaxIt];
+#pragma unroll
+    for (int u = 0; u < kMaxIt; ++u) {
+        const int c = j + 1 + lane + 64 * u;
+        a[u] = (c < k) ? row[c] : 0.0;
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int u = 0; u < kMaxIt; ++u) {
+        const int c = j + 1 + lane + 64 * u;
+        if (c < k) {
+            if (upd) {
+                a[u] -= (vr * sw[c] + wr * svp[c]);
+                row[c] = a[u];
+            }
+            acc = fma(a[u], sv[c], acc);
+        }
     }
     acc = wave_sum_dpp(acc);
-    if (lane == 0) p[r] = acc;
+    if (lane == 0) pout[r] = acc;
 }
 
 // Number of eigenvalues of the tridiagonal (d, e) strictly below x.
@@ -1259,17 +1322,17 @@ void launch_syev(const double *G, int k, double *W, double *Z, double *small, do
     } else if (k > 256 && k <= kTrdColThreads) {
         // working copy and vectors in the scratch, which the eigenvector
         // kernels below only use afterwards
-        double *A = scratch, *vb0 = scratch + static_cast<size_t>(k) * k, *vb1 = vb0 + k, *w = vb1 + k, *p = w + k;
+        double *A = scratch, *p0 = scratch + static_cast<size_t>(k) * k, *p1 = p0 + k, *w = p1 + k, *vl = w + k;
         BSQ_HIP(hipMemcpyAsync(A, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));
-        for (int j = 0; j + 2 <= k; ++j) {
-            double *vprev = (j & 1) ? vb0 : vb1, *vcur = (j & 1) ? vb1 : vb0;
-            trd_col_kernel<<<1, kTrdColThreads, 0, stream>>>(A, k, j, vprev, p, w, vcur, d, e, tau, W);
-            if (j + 3 <= k) {
-                const unsigned rows = static_cast<unsigned>(k - j - 1);
-                trd_update_kernel<<<static_cast<unsigned>(ceil_div(rows, kTrdRowsPerBlock)), 256, 0, stream>>>(
-                    A, k, j, vprev, w, vcur, p);
-            }
+        // one launch per reflector j = 0 .. k-3, then the last column
+        for (int j = 0; j + 3 <= k; ++j) {
+            const unsigned rows = static_cast<unsigned>(k - j - 1);
+            trd_step_kernel<<<static_cast<unsigned>(ceil_div(rows, kTrdStepThreads / 64)), kTrdStepThreads, 0,
+                              stream>>>(A, k, j, (j & 1) ? p0 : p1, (j & 1) ? p1 : p0, d, e, tau, W);
         }
+        const int jl = k - 2;  // p_{k-3} was written by step k-3 into ((k-3) & 1) ? p1 : p0
+        trd_col_kernel<<<1, kTrdColThreads, 0, stream>>>(A, k, jl, W + static_cast<size_t>(jl - 1) * k,
+                                                         ((jl - 1) & 1) ? p1 : p0, w, vl, d, e, tau, W);
     } else {
         reg = false;
         BSQ_HIP(hipMemcpyAsync(W, G, static_cast<size_t>(k) * k * sizeof(double), hipMemcpyDeviceToDevice, stream));

@@ -48,7 +48,7 @@ def svd_parity(A, q, it, R, tol_rec=1e-4, tol_s=1e-5):
 def test_svd_rank_above_256_matches_oracle(m, n, q, it, decay):
     """Ranks 257 .. 512 run the two-level Cholesky, the per-column
     tridiagonalisation over a global-memory working copy (linalg.hip
-    trd_col_kernel + trd_update_kernel, reflectors row-wise) and the row-wise
+    trd_step_kernel + trd_col_kernel, reflectors row-wise) and the row-wise
     back-transformation (backtransform_rows_kernel<8, 16>)."""
     A = lowrank(m, n, min(1024, m, n), decay, 0.02, seed=q)
     k = max(1, min(q, m, n))
