@@ -870,37 +870,52 @@ __global__ __launch_bounds__(256) void ns_refine_kernel(const double *__restrict
 // C = alpha op(A) op(B) + (D ? D : 0), FP64, for the k x k blocks of the
 // two-level Cholesky below (M, N, K <= a few hundred).  op(A) is M x K (A
 // stored K x M when TA), op(B) is K x N (B stored N x K when TB).  One 32 x 32
-// tile of C per workgroup of 256 lanes, 2 x 2 outputs per lane, K staged
-// through LDS 16 at a time; entries outside the operands read as zero.
+// tile of C per workgroup of 256 lanes, 2 x 2 outputs per lane.  K is staged
+// through LDS 128 at a time, every load of a chunk issued before any is
+// stored (16-deep chunks, one memory round trip each, took 30 us for a
+// 256^3 product); entries outside the operands read as zero.
+constexpr int kDgemmKc = 128;
 template <bool TA, bool TB>
 __global__ __launch_bounds__(256) void dgemm_small_kernel(int M, int N, int K, double alpha,
                                                           const double *__restrict__ A, int lda,
                                                           const double *__restrict__ B, int ldb,
                                                           const double *__restrict__ D, int ldd,
                                                           double *__restrict__ C, int ldc) {
-    __shared__ double As[16][33];  // As[kk][m]
-    __shared__ double Bs[16][33];  // Bs[kk][n]
+    __shared__ double As[kDgemmKc][33];  // As[kk][m]
+    __shared__ double Bs[kDgemmKc][33];  // Bs[kk][n]
+    constexpr int kPer = 32 * kDgemmKc / 256;  // chunk elements per lane and operand
     const int tid = threadIdx.x, m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
     const int tr = 2 * (tid >> 4), tc = 2 * (tid & 15);
     double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
-    for (int k0 = 0; k0 < K; k0 += 16) {
-        for (int t = tid; t < 512; t += 256) {
-            // element (kk, i) of the A and B chunks
-            const int kk = TA ? (t >> 5) : (t & 15), i = TA ? (t & 31) : (t >> 4);
-            const int gk = k0 + kk, gm = m0 + i, gn = n0 + i;
-            double a = 0.0, b = 0.0;
-            if (gk < K && gm < M) a = TA ? A[static_cast<uint64_t>(gk) * lda + gm] : A[static_cast<uint64_t>(gm) * lda + gk];
-            As[kk][i] = a;
-            const int kb = TB ? (t & 15) : (t >> 5), j = TB ? (t >> 4) : (t & 31);
+    for (int k0 = 0; k0 < K; k0 += kDgemmKc) {
+        // element (kk, i) of the A and B chunks: consecutive lanes read
+        // consecutive addresses in either storage order
+        double a[kPer], b[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int t = tid + 256 * q;
+            const int kk = TA ? (t >> 5) : (t & (kDgemmKc - 1)), i = TA ? (t & 31) : (t / kDgemmKc);
+            const int gk = k0 + kk, gm = m0 + i;
+            a[q] = (gk < K && gm < M)
+                       ? (TA ? A[static_cast<uint64_t>(gk) * lda + gm] : A[static_cast<uint64_t>(gm) * lda + gk])
+                       : 0.0;
+            const int kb = TB ? (t & (kDgemmKc - 1)) : (t >> 5), j = TB ? (t / kDgemmKc) : (t & 31);
             const int gkb = k0 + kb, gnb = n0 + j;
-            if (gkb < K && gnb < N)
-                b = TB ? B[static_cast<uint64_t>(gnb) * ldb + gkb] : B[static_cast<uint64_t>(gkb) * ldb + gnb];
-            Bs[kb][j] = b;
-            (void)gn;
+            b[q] = (gkb < K && gnb < N)
+                       ? (TB ? B[static_cast<uint64_t>(gnb) * ldb + gkb] : B[static_cast<uint64_t>(gkb) * ldb + gnb])
+                       : 0.0;
+        }
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int t = tid + 256 * q;
+            const int kk = TA ? (t >> 5) : (t & (kDgemmKc - 1)), i = TA ? (t & 31) : (t / kDgemmKc);
+            As[kk][i] = a[q];
+            const int kb = TB ? (t & (kDgemmKc - 1)) : (t >> 5), j = TB ? (t / kDgemmKc) : (t & 31);
+            Bs[kb][j] = b[q];
         }
         __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
+        const int kn = min(kDgemmKc, K - k0);
+        for (int kk = 0; kk < kn; ++kk) {
             const double a0 = As[kk][tr], a1 = As[kk][tr + 1], b0 = Bs[kk][tc], b1 = Bs[kk][tc + 1];
             acc[0][0] = fma(a0, b0, acc[0][0]);
             acc[0][1] = fma(a0, b1, acc[0][1]);
