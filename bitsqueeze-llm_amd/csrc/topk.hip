@@ -497,7 +497,7 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
     }
 }
 
-// Register-resident variant for rows of up to 4096 columns with cols % 4 == 0
+// Register-resident variant for rows of up to 14336 columns with cols % 4 == 0
 // and k <= 256: each lane keeps its NV4 column quads of the row in
 // VGPRs (lane t owns columns 4 (t + 256 m) .. + 3), so LDS holds only the
 // small selection arrays and many rows run per CU.  Selection as in the
@@ -993,13 +993,14 @@ void launch_reg(const TopkArgs &a, hipStream_t stream) {
 
 // Whether the register-resident kernel serves this shape: rows up to 11264
 // columns (44 values per lane, about 120 VGPRs: four rows per CU, one more
-// than the LDS-cached kernel fits); longer rows would pass 128 VGPRs and
-// halve the resident rows.
+// than the LDS-cached kernel fits), and up to 14336 columns with 56 values
+// per lane (148 VGPRs, three rows per CU, where the LDS-cached kernel holds
+// two: C5's 14336-column passes 535 -> 376 and 398 -> 238 us).
 bool reg_eligible(const TopkArgs &a) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(a.a) | reinterpret_cast<uintptr_t>(a.residual) |
                          (a.source == TopkSource::DenseMinusDense ? reinterpret_cast<uintptr_t>(a.b) : 0);
     if (a.k > kTopkMaxK || (a.cols & 3u) != 0 || (al & 15u) != 0 || a.k > kThreads || a.k > a.cols / 4) return false;
-    return ceil_div(a.cols / 4, kThreads) <= 11;
+    return ceil_div(a.cols / 4, kThreads) <= 14;
 }
 
 // True (and launched) when the register-resident kernel serves this shape.
@@ -1011,6 +1012,7 @@ bool try_launch_reg(const TopkArgs &a, hipStream_t stream) {
     else if (nv4 <= 4) launch_reg<SRC, 4>(a, stream);
     else if (nv4 <= 8) launch_reg<SRC, 8>(a, stream);
     else if (nv4 <= 11) launch_reg<SRC, 11>(a, stream);
+    else if (nv4 <= 14) launch_reg<SRC, 14>(a, stream);
     else return false;
     return true;
 }
