@@ -146,7 +146,7 @@ struct TopkArgs {
     uint16_t *indices = nullptr;      // rows x k
     float *values = nullptr;          // rows x k
     float *residual = nullptr;        // optional: a with the selected entries zeroed
-    uint32_t *flags = nullptr;        // optional: OR kFlagError if any |v| > FLT_EPSILON
+    uint32_t *flags = nullptr;        // optional: set to kFlagError if any |v| > FLT_EPSILON (the word holds 0 or kFlagError)
     // optional, with `residual`: row_gmax[r] = max over the residual's
     // 64-element blocks of row r of the block's largest sanitised |value|
     // (1 for an all-zero block), the per-row part of NF4_DQ's global scale

@@ -28,6 +28,16 @@ namespace {
 constexpr int kThreads = 256;
 constexpr uint32_t kCacheMaxCols = 16384;  // 64 KiB of LDS row cache
 
+// Marks the error section present.  During a compress the flags word holds
+// 0 or kFlagError (cleared before the pass, set only here), so every row that
+// finds an entry above FLT_EPSILON stores the same value: a relaxed store at
+// workgroup scope, merged in each XCD's L2 and visible once the kernel ends.
+// A device-scope atomicOr per row serialises at the memory side instead
+// (about 10 ns apiece: 8192 rows added 78 us to a 21 us launch).
+__device__ __forceinline__ void set_error_flag(uint32_t *flags) {
+    __hip_atomic_store(flags, kFlagError, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 __device__ __forceinline__ uint32_t order_key(float v) {
     // |v| as an ordered integer, NaN below +0 (build_sort_inputs_kernel maps
     // NaN to -inf, topk_cuda_utils.cuh:62-66).
@@ -263,7 +273,7 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(TopkArgs a) {
             nonzero |= fabsf(load_value<SRC>(a, sh.L, dq, row0 + c)) > FLT_EPSILON;
     }
     if (a.flags && __syncthreads_or(nonzero ? 1 : 0)) {
-        if (threadIdx.x == 0) atomicOr(a.flags, kFlagError);
+        if (threadIdx.x == 0) set_error_flag(a.flags);
     }
     __syncthreads();
 
@@ -659,7 +669,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     const uint32_t key32 = mx >= 0.0f ? __float_as_uint(mx) + 1u : 0u;
     const bool nonzero = mx > FLT_EPSILON;  // false for NaN-only and padding lanes
     if (a.flags && __syncthreads_or(nonzero ? 1 : 0)) {
-        if (tid == 0) atomicOr(a.flags, kFlagError);
+        if (tid == 0) set_error_flag(a.flags);
     }
     // filter threshold: the top 16 bits of the k-th largest lane maximum's
     // order key, by two 8-bit radix passes over one key per lane (k lanes
@@ -906,7 +916,7 @@ __global__ __launch_bounds__(kThreads) void topk_band_kernel(TopkArgs a) {
         nonzero |= fabsf(v) > FLT_EPSILON;
     }
     if (a.flags && blockIdx.y == 0 && __syncthreads_or(nonzero ? 1 : 0)) {
-        if (threadIdx.x == 0) atomicOr(a.flags, kFlagError);
+        if (threadIdx.x == 0) set_error_flag(a.flags);
     }
     __syncthreads();
     auto value_at = [&](uint32_t c) -> float {
