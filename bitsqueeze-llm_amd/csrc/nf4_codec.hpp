@@ -66,6 +66,41 @@ __device__ __forceinline__ uint32_t nf4_code_small(const Nf4Table &t, float v) {
     return e.y + ((v >= __uint_as_float(e.x)) ? 1u : 0u);
 }
 
+// The same bins with the two candidate levels of each: (bits of the
+// threshold, code_lo, L[code_lo], L[code_lo + 1]) in one 16-byte entry, so an
+// encoder that also needs the level of the code (the fused encode + error
+// pass) reads both with one lookup.
+struct Nf4LevelTable {
+    uint4 ent[256];
+};
+
+__device__ __forceinline__ void nf4_level_table_build(Nf4LevelTable &t) {
+    constexpr float T[15] = BSQ_NF4_THRESHOLDS;
+    constexpr float L[16] = BSQ_NF4_LEVELS;
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+        const float e0 = -1.0f + static_cast<float>(b) / 128.0f, e1 = -1.0f + static_cast<float>(b + 1) / 128.0f;
+        uint32_t lo = 0;
+        float thr = __builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 15; ++i) {
+            lo += (T[i] <= e0) ? 1u : 0u;
+            if (T[i] > e0 && T[i] < e1) thr = T[i];
+        }
+        // a bin whose code_lo is 15 holds no threshold (thr = inf): its upper
+        // level is never taken
+        t.ent[b] = uint4{__float_as_uint(thr), lo, __float_as_uint(L[lo]), __float_as_uint(L[lo < 15 ? lo + 1 : 15])};
+    }
+}
+
+// code of v (|v| < 2, as nf4_code_small) and its level L[code]
+__device__ __forceinline__ uint32_t nf4_code_level_small(const Nf4LevelTable &t, float v, float &level) {
+    const int b = min(max(static_cast<int>((v + 1.0f) * 128.0f), 0), 255);
+    const uint4 e = t.ent[b];
+    const bool up = v >= __uint_as_float(e.x);
+    level = __uint_as_float(up ? e.w : e.z);
+    return e.y + (up ? 1u : 0u);
+}
+
 __device__ __forceinline__ uint32_t nf4_code(const Nf4Table &t, float v) {
     if (fabsf(v) < 2.0f) return nf4_code_small(t, v);
     return nf4_code_scan(v);

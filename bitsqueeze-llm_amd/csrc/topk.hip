@@ -518,7 +518,7 @@ template <TopkSource SRC, int NV4>
 __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     constexpr bool ENC = SRC == TopkSource::EncodeNF4 || SRC == TopkSource::EncodeNF4DQ;
     __shared__ Shared sh;
-    __shared__ Nf4Table etab;  // encode sources: the NF4 code table (unused, and dropped, otherwise)
+    __shared__ Nf4LevelTable etab;  // encode sources: the NF4 code and level table (unused, and dropped, otherwise)
     __shared__ __attribute__((aligned(16))) unsigned long long bk[kFastCap];
     __shared__ float bv[kFastCap];
     const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
@@ -540,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         if (dq == 0.0f || !__builtin_isfinite(dq)) dq = 1.0f;
     }
     if constexpr (ENC) {
-        nf4_table_build(etab);
+        nf4_level_table_build(etab);
         if constexpr (SRC == TopkSource::EncodeNF4DQ) {
             const float raw = dq_raw_from_gmax(*a.enc_gmax);
             dq = dq_effective(raw);
@@ -624,8 +624,26 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
             }
             const float inv = 1.0f / scale;
             uint32_t c[4];
+            // |w| < 2 unless a block scale fell far below the block's absmax
+            // (an NF4_DQ scale code of 0 replaced by 1): the table path for
+            // the whole quad, the exact scan only for such quads
+            float w[4], lv[4];
+            bool small = true;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) c[u] = nf4_code(etab, sv[u] * inv);
+            for (int u = 0; u < 4; ++u) {
+                w[u] = sv[u] * inv;
+                small = small && (fabsf(w[u]) < 2.0f);
+            }
+            if (small) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) c[u] = nf4_code_level_small(etab, w[u], lv[u]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    c[u] = (fabsf(w[u]) < 2.0f) ? nf4_code_level_small(etab, w[u], lv[u]) : nf4_code_scan(w[u]);
+                    lv[u] = sh.L[c[u]];
+                }
+            }
             const uint64_t e = row0 + 4ull * c4;
             if (inside) {
                 *reinterpret_cast<uint16_t *>(a.enc_codes + (e >> 1)) =
@@ -636,7 +654,7 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[m][u] = inside ? v[m][u] - scale * sh.L[c[u]] : __builtin_nanf("");
+            for (int u = 0; u < 4; ++u) v[m][u] = inside ? v[m][u] - scale * lv[u] : __builtin_nanf("");
         }
     }
     // keys are recomputed from the values in every phase (an opaque copy of

@@ -237,6 +237,28 @@ def test_device_resident_matches_abi(fmt, ro, re):
     B.decompress_release()
 
 
+@pytest.mark.parametrize("ro", [0.0, 0.02])
+def test_fused_encode_blocks_below_the_scale_range(ro):
+    """NF4_DQ blocks far below the global maximum get E4M3 scale code 0,
+    replaced by 1, so their scaled values leave the table's |w| < 2 range and
+    take the exact nearest-level scan inside the fused encode + error pass
+    (cols % 64 == 0, with and without the selection bitmap of an outlier
+    separation); bytes and decode equal the oracle's."""
+    rows, cols = 16, 1024
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[0] *= 1e9                                  # sets the global scale
+    x[3, :64] *= 1e-3                            # blocks at, below and far below the E4M3 range
+    x[5, 128:256] *= 1e-7
+    x[7, 512:576] = np.float32(1e-30)
+    data, out, _ = run_direct(x, ro, 0.05, B.NF4_DQ)
+    exp_bytes, exp_out = oracle_direct(x, ro, 0.05, B.NF4_DQ)
+    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+    assert out.tobytes() == exp_out.tobytes()
+    B.compress_release()
+    B.decompress_release()
+
+
 def _device_flags(packed):
     out = np.zeros(1, np.uint32)
     B.check(B.lib().bsq_memcpy_d2h(out.ctypes.data_as(C.c_void_p), C.c_void_p(packed.d_flags), 4), "D2H")
