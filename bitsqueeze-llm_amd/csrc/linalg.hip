@@ -526,6 +526,18 @@ __global__ __launch_bounds__(kTrdStepThreads) void trd_step_kernel(
     const int i = threadIdx.x;
     const bool in = i < k;
     const bool lead = blockIdx.x == 0;
+    // this wave's trailing row, requested first: its loads do not depend on
+    // the reflector, so their latency overlaps the two reductions below
+    const int lane = i & 63;
+    const int r = j + 1 + static_cast<int>(blockIdx.x) * (kTrdStepThreads / 64) + (i >> 6);
+    constexpr int kMaxIt = kTrdStepThreads / 64;  // k <= 512: at most 8 columns per lane
+    double *row = A + static_cast<uint64_t>(r < k ? r : j) * k;
+    double a[kMaxIt];
+#pragma unroll
+    for (int u = 0; u < kMaxIt; ++u) {
+        const int c = j + 1 + lane + 64 * u;
+        a[u] = (r < k && c < k) ? row[c] : 0.0;
+    }
     // w_{j-1} on indices >= j (zero below); v_{j-1} is row j-1 of H
     double wi = 0.0, vpi = 0.0;
     if (j > 0) {
@@ -567,19 +579,9 @@ __global__ __launch_bounds__(kTrdStepThreads) void trd_step_kernel(
     }
     __syncthreads();
     // trailing rows: update j-1, then p_j = A v_j
-    const int lane = i & 63;
-    const int r = j + 1 + static_cast<int>(blockIdx.x) * (kTrdStepThreads / 64) + (i >> 6);
     if (r >= k) return;  // whole waves, after the last barrier
     const bool upd = j > 0;
     const double vr = svp[r], wr = sw[r];
-    double *row = A + static_cast<uint64_t>(r) * k;
-    constexpr int kMaxIt = kTrdStepThreads / 64;  // k <= 512: at most 8 columns per lane
-    double a[kMaxIt];
-#pragma unroll
-    for (int u = 0; u < kMaxIt; ++u) {
-        const int c = j + 1 + lane + 64 * u;
-        a[u] = (c < k) ? row[c] : 0.0;
-    }
     double acc = 0.0;
 #pragma unroll
     for (int u = 0; u < kMaxIt; ++u) {
