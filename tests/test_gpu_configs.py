@@ -44,6 +44,7 @@ def svd_parity(A, q, it, R, tol_rec=1e-4, tol_s=1e-5):
     (1200, 3000, 257, 2, 1.0),   # one past the register-resident kernels, transposed branch
     (2600, 1100, 300, 1, 1.2),   # m > n branch
     (2048, 14336, 512, 3, 0.8),  # C5's rank and iterations on its 8-way row share
+    (900, 1500, 449, 1, 1.1),    # an odd rank: the per-column kernels' last lanes idle
 ])
 def test_svd_rank_above_256_matches_oracle(m, n, q, it, decay):
     """Ranks 257 .. 512 run the two-level Cholesky, the per-column

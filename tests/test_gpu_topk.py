@@ -66,13 +66,14 @@ def test_ties_nan_inf_zero_rows():
         _check(x, k)
 
 
-@pytest.mark.parametrize("cols", [600, 4096, 8000, 11008, 14336, 20000])
+@pytest.mark.parametrize("cols", [600, 4096, 8000, 11008, 12000, 14336, 16000, 20000])
 def test_ties_at_threshold_every_kernel(cols):
     """Heavy ties in magnitude (integers -3..3 and their negatives, so equal
     |v| sits on both sides of the k-th entry), NaN / inf / +-0 / subnormal
-    rows, at widths served by each kernel variant (register rows of 2, 4, 8
-    and 11 quads, the LDS-cached and the uncached kernel); the separation
-    residual zeroes exactly the selected entries."""
+    rows, at widths served by each kernel variant (register rows of 2, 4, 8,
+    11 and 14 quads per lane, the last also part-filled at 12000 columns,
+    then the LDS-cached kernel at 16000 and the uncached one at 20000); the
+    separation residual zeroes exactly the selected entries."""
     rng = np.random.default_rng(cols)
     x = rng.integers(-3, 4, (12, cols)).astype(np.float32)
     x[0] = 0.0
