@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <limits>
+#include <malloc.h>
 #include <memory>
 #include <mutex>
 #include <thread>
@@ -149,6 +150,53 @@ class CopyPool {
 void host_copy(void *dst, const void *src, size_t n) { CopyPool::get().copy(dst, src, n); }
 // zeroes (and so faults in) a fresh host block with the same threads
 void host_touch(void *dst, size_t n) { CopyPool::get().copy(dst, nullptr, n); }
+
+// Packed objects handed back through bitsqz_llm_free are kept for the next
+// compress (at most two, 1 GiB in total, blocks of 1 MiB and more): a fresh
+// calloc block of that size is mapped lazily and takes a page fault per
+// 4 KB on first touch, which a reused block has already taken.  They are
+// malloc blocks, so a caller that releases an object with free() instead
+// stays correct (that block is simply not kept).
+class BlockCache {
+  public:
+    static BlockCache &get() {
+        static BlockCache cache;
+        return cache;
+    }
+    // a kept block of n bytes or a little more, or null
+    void *take(size_t n) {
+        std::lock_guard<std::mutex> lock(mu_);
+        for (size_t i = 0; i < blocks_.size(); ++i) {
+            const size_t cap = blocks_[i].second;
+            if (cap >= n && cap <= n + n / 2) {
+                void *p = blocks_[i].first;
+                bytes_ -= cap;
+                blocks_.erase(blocks_.begin() + static_cast<std::ptrdiff_t>(i));
+                return p;
+            }
+        }
+        return nullptr;
+    }
+    // true when the block is kept (the caller frees it otherwise)
+    bool put(void *p) {
+        const size_t cap = malloc_usable_size(p);
+        if (cap < kMinBytes) return false;
+        std::lock_guard<std::mutex> lock(mu_);
+        if (blocks_.size() >= kMaxBlocks || bytes_ + cap > kMaxBytes) return false;
+        blocks_.emplace_back(p, cap);
+        bytes_ += cap;
+        return true;
+    }
+    ~BlockCache() {
+        for (auto &b : blocks_) std::free(b.first);
+    }
+
+  private:
+    static constexpr size_t kMinBytes = size_t{1} << 20, kMaxBytes = size_t{1} << 30, kMaxBlocks = 2;
+    std::mutex mu_;
+    std::vector<std::pair<void *, size_t>> blocks_;
+    size_t bytes_ = 0;
+};
 
 void set_error(const char *msg) { g_last_error = msg ? msg : ""; }
 
@@ -944,13 +992,17 @@ bitsqz_llm_array_t *assemble_host(Runtime &rt, const bsq_device_packed_t &P) {
     // the host object, sized for every section (the error blob's presence is
     // decided last; a smaller object leaves the tail unused), filled group by
     // group while the device still works on the later ones
-    std::unique_ptr<void, void (*)(void *)> block(std::calloc(1, 200 + full), std::free);
+    void *raw = BlockCache::get().take(200 + full);
+    const bool reused = raw != nullptr;
+    if (!reused) raw = std::calloc(1, 200 + full);
+    std::unique_ptr<void, void (*)(void *)> block(raw, std::free);
     BSQ_REQUIRE(block != nullptr, "calloc of the packed object failed");
     uint8_t *pl = static_cast<uint8_t *>(block.get()) + 200;
     // calloc maps a large block lazily: its pages are faulted in by several
     // threads while the copies above are still in flight, so the copies
-    // below run without faults
-    host_touch(pl, full);
+    // below run without faults (a reused block has its pages already; every
+    // byte of it up to the object's end is written below)
+    if (!reused) host_touch(pl, full);
     auto put_topk = [&](int t) {
         const bitsqz_section_t &d = *descs[4 + t];
         if (d.storage == BITSQZ_SECTION_NONE) return;
@@ -988,6 +1040,9 @@ bitsqz_llm_array_t *assemble_host(Runtime &rt, const bsq_device_packed_t &P) {
         H.flags |= kFlagError;
         put_topk(1);
     } else {
+        // the error blob's space stays as calloc leaves it
+        const bitsqz_section_t &d = *descs[5];
+        if (reused && d.storage != BITSQZ_SECTION_NONE) host_copy(pl + d.offset, nullptr, d.size);
         H.section_error_topk = bitsqz_section_t{};
     }
     auto *buf = static_cast<bitsqz_llm_array_t *>(block.release());
@@ -1446,7 +1501,7 @@ bitsqz_llm_array_t *load_bitsqz_llm_from_buffer(const void *buffer, uint64_t buf
 
 void bitsqz_llm_free(bitsqz_llm_array_t *compressed) {
     if (!compressed) return;
-    std::free(compressed);
+    if (!BlockCache::get().put(compressed)) std::free(compressed);
 }
 
 // topk_compute_num_topk_columns: exported because the reference's ABI tests
