@@ -128,9 +128,9 @@ def abi_leg(src, ddst, n, wl, reps=5):
     times = []
     for i in range(reps + 1):
         out = C.POINTER(B.PackedHeader)()
-        prof = B.Profile()
         t0 = time.perf_counter()
-        B.check(L.bsq_compress(src_ptr, C.byref(out), C.byref(prof)), "bitsqz_llm_compress")
+        # no profile struct: the reference's two-argument bitsqz_llm_compress
+        B.check(L.bsq_compress(src_ptr, C.byref(out), None), "bitsqz_llm_compress")
         B.check(L.bsq_decompress(C.cast(out, C.c_void_p), ddst.ptr, n), "bitsqz_llm_decompress")
         dt = time.perf_counter() - t0
         L.bsq_free(C.cast(out, C.c_void_p))

@@ -574,15 +574,21 @@ void decompress_init(Runtime &rt, uint16_t rows, uint16_t cols, float r_out, flo
     rt.initialized = true;
 }
 
+// stage events recorded by compress_device
+enum : int { kNoEvents = 0, kCopyEvents = 1, kAllEvents = 2 };
+
 // The device-resident compress pipeline (src/bitsqz_llm.cu:981-1247 without
 // the host copies).  Everything is enqueued on rt.stream.
-void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, const bool stage_events) {
+void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, const int stage_events) {
     const hipStream_t st = rt.stream;
-    // stage boundaries for the host path (its copy stream waits on them, and
-    // the profile reports their spans); each record costs the queue a few
-    // microseconds of idle time, so the device-resident path skips them
+    // stage boundaries: the host path's copy stream waits on ev[1] (after
+    // the separation), ev[3] (after the encode) and ev[6] (the end), and a
+    // requested profile reports the spans of all of them.  Each record costs
+    // the queue a few microseconds of idle time, so only those needed are
+    // recorded (none on the device-resident path).
     auto mark = [&](int i) {
-        if (stage_events) BSQ_HIP(hipEventRecord(rt.ev[i], st));
+        if (stage_events == kAllEvents || (stage_events == kCopyEvents && (i == 1 || i == 3 || i == 6)))
+            BSQ_HIP(hipEventRecord(rt.ev[i], st));
     };
     const uint32_t rows = rt.rows, cols = rt.cols;
     const uint64_t N = static_cast<uint64_t>(rows) * cols;
@@ -1403,18 +1409,20 @@ int bitsqz_llm_compress(const float *row_major_matrix_float_data, bitsqz_llm_arr
         const float *d_in = row_major_matrix_float_data;
         const hipEvent_t t_begin = rt.t_begin, t_end = rt.t_end;
         {
-            BSQ_HIP(hipEventRecord(t_begin, rt.stream));
+            if (profile) BSQ_HIP(hipEventRecord(t_begin, rt.stream));
             if (rt.input_location == BITSQZ_LLM_INPUT_HOST) {
                 BSQ_HIP(hipMemcpyAsync(rt.d_stage, row_major_matrix_float_data, N * 4, hipMemcpyHostToDevice,
                                        rt.stream));
                 d_in = rt.d_stage;
             }
             bsq_device_packed_t P{};
-            compress_device(rt, d_in, &P, true);
+            compress_device(rt, d_in, &P, profile ? kAllEvents : kCopyEvents);
+            // assemble_host returns once the copy stream has passed ev[6],
+            // the end of the compute: nothing is left in flight
             bitsqz_llm_array_t *buf = assemble_host(rt, P);
-            BSQ_HIP(hipEventRecord(t_end, rt.stream));
-            BSQ_HIP(hipEventSynchronize(t_end));
             if (profile) {
+                BSQ_HIP(hipEventRecord(t_end, rt.stream));
+                BSQ_HIP(hipEventSynchronize(t_end));
                 auto ms = [](hipEvent_t a, hipEvent_t b) {
                     float v = 0.0f;
                     return hipEventElapsedTime(&v, a, b) == hipSuccess ? static_cast<double>(v) : 0.0;
@@ -1560,7 +1568,7 @@ int bsq_device_compress(const float *d_input, bsq_device_packed_t *out) {
         set_error("bsq_device_compress: runtime not initialised or null argument");
         return 1;
     }
-    return guarded([&] { compress_device(g_comp, d_input, out, false); });
+    return guarded([&] { compress_device(g_comp, d_input, out, kNoEvents); });
 }
 
 int bsq_device_decompress(const bsq_device_packed_t *packed, float *d_dst, uint32_t dst_num_elements) {
@@ -1660,7 +1668,7 @@ int bsq_lanes_roundtrip(int lane, const float *d_input, float *d_dst) {
     }
     return guarded([&] {
         Lane &l = *g_lanes[lane];
-        compress_device(l.comp, d_input, &l.last, false);
+        compress_device(l.comp, d_input, &l.last, kNoEvents);
         decompress_device(l.decomp, l.last, l.last.topk_k[1] > 0, d_dst, l.comp.stream, l.last.d_flags);
     });
 }
