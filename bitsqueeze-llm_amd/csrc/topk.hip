@@ -521,6 +521,8 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     __shared__ Nf4LevelTable etab;  // encode sources: the NF4 code and level table (unused, and dropped, otherwise)
     __shared__ __attribute__((aligned(16))) unsigned long long bk[kFastCap];
     __shared__ float bv[kFastCap];
+    // the row's selected columns, one bit each (separation: residual, bitmap)
+    __shared__ uint32_t rowbits[NV4 * 32];
     const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
     const uint32_t r = blockIdx.x, tid = threadIdx.x;
     const uint64_t row0 = static_cast<uint64_t>(r) * cols;
@@ -534,6 +536,9 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         sh.ncand = 0;
         if (a.flags_reset && r == 0) *a.flags_reset = 0u;
     }
+    const bool separate = a.residual || a.sel_bits;  // uniform
+    if (separate)
+        for (uint32_t w = tid; w < NV4 * 32; w += kThreads) rowbits[w] = 0u;
     float dq = 1.0f;
     if constexpr (SRC == TopkSource::DenseMinusNF4DQ) {
         dq = *a.dq;
@@ -819,41 +824,38 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         const unsigned long long mine = bk[i];
         const uint32_t rank = count_greater(bk, total, mine);
         if (rank < k) {
-            out_idx[rank] = static_cast<uint16_t>(0xFFFFu - static_cast<uint32_t>(mine & 0xFFFFu));
+            const uint32_t col = 0xFFFFu - static_cast<uint32_t>(mine & 0xFFFFu);
+            out_idx[rank] = static_cast<uint16_t>(col);
             out_val[rank] = bv[i];
-            if (rank == k - 1) sh.kth = mine;
+            if (separate) atomicOr(&rowbits[col >> 5], 1u << (col & 31u));
         }
     }
-    if (a.residual || a.sel_bits) {  // uniform
+    if (separate) {
+        // the selected entries from the row's bitmap in LDS (set by the
+        // ranking above: one bit test per element instead of a key
+        // comparison)
         __syncthreads();
-        const unsigned long long kth = sh.kth;
+        if (a.sel_bits)  // cols % 64 == 0: whole words
+            for (uint32_t w = tid; w < cols / 32; w += kThreads) a.sel_bits[(row0 >> 5) + w] = rowbits[w];
         float4 *res4 = a.residual ? reinterpret_cast<float4 *>(a.residual + row0) : nullptr;
         lt = lane_id();
-        const bool kth_number = (kth >> 16) != 0;  // uniform: the k-th largest is a number
-        const MagThreshold mk(kth_number ? kth : (1ull << 16));
         // with row_gmax (cols % 64 == 0): a 64-element block is the quads of
         // 16 consecutive lanes (one DPP row) at one m, its absmax a 4-step
         // DPP max
         float gm = 0.0f;
+        if (a.residual || a.row_gmax)  // uniform
 #pragma unroll
         for (int m = 0; m < NV4; ++m) {
             const uint32_t c4 = lt + kThreads * m;
-            bool s[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) s[u] = kth_number ? mk.reaches(v[m][u], 4 * c4 + u) : (key_of(lt, m, u) >= kth);
+            // columns 4 c4 .. 4 c4 + 3: bits 4 (c4 % 8) .. + 3 of word c4 / 8
+            const uint32_t nib = rowbits[min(c4 >> 3, static_cast<uint32_t>(NV4 * 32 - 1))] >> (4u * (c4 & 7u));
             float4 o;
-            o.x = s[0] ? 0.0f : v[m][0];
-            o.y = s[1] ? 0.0f : v[m][1];
-            o.z = s[2] ? 0.0f : v[m][2];
-            o.w = s[3] ? 0.0f : v[m][3];
+            o.x = (nib & 1u) ? 0.0f : v[m][0];
+            o.y = (nib & 2u) ? 0.0f : v[m][1];
+            o.z = (nib & 4u) ? 0.0f : v[m][2];
+            o.w = (nib & 8u) ? 0.0f : v[m][3];
             if (a.residual) {  // uniform
                 if (c4 < q4) res4[c4] = o;
-            } else {
-                // the 8 lanes of an aligned group hold 32 consecutive columns
-                // (cols % 64 == 0): one bitmap word, its nibbles OR-ed together
-                const uint32_t nib = (s[0] ? 1u : 0u) | (s[1] ? 2u : 0u) | (s[2] ? 4u : 0u) | (s[3] ? 8u : 0u);
-                const uint32_t w = group8_or(nib << (4u * (c4 & 7u)));
-                if ((c4 & 7u) == 0 && c4 < q4) a.sel_bits[(row0 >> 5) + (c4 >> 3)] = w;
             }
             if (a.row_gmax) {  // uniform
                 auto san = [](float x) { return __builtin_isfinite(x) ? fabsf(x) : 0.0f; };

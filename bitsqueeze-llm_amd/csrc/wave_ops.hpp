@@ -64,13 +64,4 @@ __device__ __forceinline__ float row16_max(float v) {
     return v;
 }
 
-// bitwise OR over each aligned group of 8 lanes, in every lane of the
-// group; all 8 lanes must be active.
-__device__ __forceinline__ uint32_t group8_or(uint32_t v) {
-    v |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
-    v |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
-    v |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
-    return v;
-}
-
 }  // namespace bsq
