@@ -442,9 +442,8 @@ def main():
                     help="measure the legacy formats' device codecs instead of the packed-object pipeline")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build runs on one GPU only; the multi-GPU design (row shards, one "
-              "all-reduce per NF4_DQ section and per power iteration) is described in DESIGN.md",
-              file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (a multi-GPU run would shard rows, with one "
+              "all-reduce per NF4_DQ section and per power iteration; not built)", file=sys.stderr)
         sys.exit(2)
     if args.legacy:
         legacy_bench(args)
