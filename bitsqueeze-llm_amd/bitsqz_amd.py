@@ -334,13 +334,13 @@ def compress(src, profile: bool = False):
     """bitsqz_llm_compress: `src` is a host float32 array (HOST runtime) or a
     DeviceBuffer (DEVICE runtime).  Returns the packed bytes (and profile)."""
     out = C.POINTER(PackedHeader)()
-    prof = Profile()
+    prof = Profile() if profile else None  # no struct: the two-argument form
     if isinstance(src, DeviceBuffer):
         p = src.ptr
     else:
         src = np.ascontiguousarray(src, np.float32)
         p = _ptr(src)
-    check(lib().bsq_compress(p, C.byref(out), C.byref(prof)), "bitsqz_llm_compress")
+    check(lib().bsq_compress(p, C.byref(out), C.byref(prof) if profile else None), "bitsqz_llm_compress")
     try:
         data = packed_bytes(out)
     finally:

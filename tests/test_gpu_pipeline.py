@@ -259,6 +259,34 @@ def test_fused_encode_blocks_below_the_scale_range(ro):
     B.decompress_release()
 
 
+def test_reused_host_objects_alternating_error_sections():
+    """Packed objects freed with bitsqz_llm_free are reused by the next
+    compress: alternating an input with an error section and one the codec
+    reproduces exactly (no error section, a smaller object in the same
+    block), with and without a profile struct, every object equals the
+    oracle's bytes and decodes like it (objects of about 1.8 MB: large
+    enough to be kept)."""
+    rows, cols = 1024, 2048
+    rng = np.random.default_rng(21)
+    x_err = rng.standard_normal((rows, cols)).astype(np.float32)
+    x_exact = np.tile(np.array([1.0, -1.0, 0.0, 0.5626170039176941], np.float32), (rows, cols // 4))
+    B.compress_release()
+    B.decompress_release()
+    assert B.compress_initialize(rows, cols, 0.0, 0.05, -1, 2, B.QUANT_NONE, B.QUANT_NONE, B.NF4, B.INPUT_HOST) == 0
+    assert B.decompress_initialize(rows, cols, 0.0, 0.05, -1, B.QUANT_NONE, B.QUANT_NONE, B.NF4) == 0
+    expect = {name: oracle_direct(x, 0.0, 0.05, B.NF4) for name, x in (("err", x_err), ("exact", x_exact))}
+    assert len(expect["exact"][0]) < len(expect["err"][0])
+    for i in range(6):
+        name, x = ("err", x_err) if i % 2 == 0 else ("exact", x_exact)
+        got = B.compress(x, profile=(i % 3 == 0))
+        data = got[0] if isinstance(got, tuple) else got
+        assert O.mask_pointer(data) == O.mask_pointer(expect[name][0]), (i, name)
+        out = B.decompress(data, rows, cols)
+        assert out.tobytes() == expect[name][1].tobytes(), (i, name)
+    B.compress_release()
+    B.decompress_release()
+
+
 def _device_flags(packed):
     out = np.zeros(1, np.uint32)
     B.check(B.lib().bsq_memcpy_d2h(out.ctypes.data_as(C.c_void_p), C.c_void_p(packed.d_flags), 4), "D2H")
