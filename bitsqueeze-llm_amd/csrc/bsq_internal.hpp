@@ -95,8 +95,10 @@ void launch_quant_encode(const float *x, uint64_t n, int method, float *scales_f
 void launch_nf4dq_gmax(const float *x, uint64_t n, uint8_t *codes, uint32_t *gmax, hipStream_t stream);
 void launch_rows_gmax(const float *row_gmax, uint32_t rows, uint32_t *gmax, hipStream_t stream);
 // NF4_DQ encode whose global max of the block absmax is already known per row
-// (row_gmax[0 .. rows), from the outlier separation): one small reduce, then
-// the encode pass; the same bytes as launch_quant_encode.
+// (row_gmax[0 .. rows), from the outlier separation): the encode pass, whose
+// workgroups reduce the maxima themselves when rows <= kInlineGmaxRows and
+// rows % 4 == 0 (else one small reduce launch first); the same bytes as
+// launch_quant_encode.
 void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gmax, uint32_t rows,
                                  uint8_t *scales_u8, float *dq_out, uint8_t *codes, uint32_t *gmax_scratch,
                                  hipStream_t stream, const uint8_t *sel = nullptr);
@@ -163,6 +165,11 @@ struct TopkArgs {
     uint8_t *enc_scales_u8 = nullptr;
     const uint32_t *enc_gmax = nullptr;
     float *enc_dq_out = nullptr;
+    // EncodeNF4DQ, in place of enc_gmax: the per-row maxima of a separation
+    // (row_gmax above; enc_gmax_rows of them, a multiple of 4 up to
+    // kInlineGmaxRows, 16-byte aligned), reduced by every workgroup itself
+    const float *enc_row_gmax = nullptr;
+    uint32_t enc_gmax_rows = 0;
     // separation without a residual (Dense source, the register-resident
     // kernel, cols % 64 == 0): bit (r * cols + c) of sel_bits (32-bit words,
     // bit i of word w = element 32 w + i) is set when column c of row r is
@@ -175,6 +182,9 @@ struct TopkArgs {
     // loads allocate in the caches (otherwise they are non-temporal)
     bool keep_input = false;
 };
+// Most per-row maxima the fused NF4_DQ encode reduces in every workgroup
+// (TopkArgs::enc_row_gmax): four 16-byte loads per lane.
+constexpr uint32_t kInlineGmaxRows = 4096;
 // True when the fused encode + top-k pass (TopkSource::EncodeNF4 / EncodeNF4DQ)
 // serves this shape: the register-resident kernel's shapes with cols % 64 == 0.
 bool topk_encode_supported(uint32_t rows, uint32_t cols, uint32_t k, const float *a, const uint8_t *codes);

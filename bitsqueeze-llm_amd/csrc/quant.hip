@@ -132,12 +132,18 @@ __global__ __launch_bounds__(kThreads) void dq_gmax_kernel(const float *__restri
 // SEL: sel[chunk] flags the chunk's elements that a separation took out
 // (bit i = element 8 chunk + i); they are encoded as 0, as the residual
 // holds them.
+// NF4_DQ: the global scale comes from *gmax, or, when row_gmax is given,
+// from the largest of row_gmax[0 .. gmax_rows) (a separation's per-row
+// maxima; gmax_rows a multiple of 4 up to kInlineGmaxRows), which every
+// workgroup reduces itself.
 template <bool DQ, bool SEL>
 __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     const float *__restrict__ x, uint64_t n, bool vec_ok, float *__restrict__ scales_f32,
-    uint8_t *__restrict__ scales_u8, const uint32_t *__restrict__ gmax, float *__restrict__ dq_out,
-    uint8_t *__restrict__ codes, uint32_t *__restrict__ flags_reset, const uint8_t *__restrict__ sel) {
+    uint8_t *__restrict__ scales_u8, const uint32_t *__restrict__ gmax, const float *__restrict__ row_gmax,
+    uint32_t gmax_rows, float *__restrict__ dq_out, uint8_t *__restrict__ codes,
+    uint32_t *__restrict__ flags_reset, const uint8_t *__restrict__ sel) {
     __shared__ Nf4Table tab;
+    __shared__ float gwmax[kThreads / 64];
     // the pipeline's flags word, cleared here when no earlier kernel of the
     // compress does it (saves a fill launch); nothing reads it before this
     // kernel ends
@@ -225,13 +231,32 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
     // work and the barrier overlap the first memory round trip
     if (base < nchunks) load_it(base, va, sa);
     if (base + step < nchunks) load_it(base + step, vb, sbb);
-    nf4_table_build(tab);
     if constexpr (DQ) {
-        const float raw = dq_raw_from_gmax(*gmax);
+        if (row_gmax) {  // uniform: wave maxima of the per-row maxima to LDS
+            constexpr int kGq = kInlineGmaxRows / (4 * kThreads);
+            float gm = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kGq; ++j) {
+                const uint32_t i4 = threadIdx.x + kThreads * j;
+                if (4 * i4 < gmax_rows) {
+                    const f32x4 g = reinterpret_cast<const f32x4 *>(row_gmax)[i4];
+                    gm = fmaxf(gm, fmaxf(fmaxf(g.x, g.y), fmaxf(g.z, g.w)));
+                }
+            }
+            for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+            if ((threadIdx.x & 63) == 0) gwmax[threadIdx.x >> 6] = gm;
+        }
+    }
+    nf4_table_build(tab);
+    __syncthreads();
+    if constexpr (DQ) {
+        // max is order-free: every workgroup gets the same bits
+        const uint32_t gbits =
+            row_gmax ? __float_as_uint(fmaxf(fmaxf(gwmax[0], gwmax[1]), fmaxf(gwmax[2], gwmax[3]))) : *gmax;
+        const float raw = dq_raw_from_gmax(gbits);
         dq = dq_effective(raw);
         if (blockIdx.x == 0 && threadIdx.x == 0) *dq_out = raw;
     }
-    __syncthreads();
     for (bool first = true; base < nchunks; base += 2 * step, first = false) {  // uniform
         if (!first && base + step < nchunks) load_it(base + step, vb, sbb);
         encode_it(base, va, sa);
@@ -504,16 +529,22 @@ namespace {
 // a round of five and a round of three (supplement encode 54.5 -> 50.5 us).
 template <bool DQ>
 void encode_pass(const float *x, uint64_t n, float *scales_f32, uint8_t *scales_u8, const uint32_t *gmax,
-                 float *dq_out, uint8_t *codes, uint32_t *flags_reset, const uint8_t *sel, hipStream_t stream) {
+                 float *dq_out, uint8_t *codes, uint32_t *flags_reset, const uint8_t *sel, hipStream_t stream,
+                 const float *row_gmax = nullptr, uint32_t gmax_rows = 0) {
     const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
     const unsigned grid = grid_for(ceil_div(n, 8), 5);
     BSQ_REQUIRE(!sel || n % kQuantBlock == 0, "quant encode: a selection bitmap needs whole blocks");
+    BSQ_REQUIRE(!row_gmax || (DQ && gmax_rows > 0 && gmax_rows % 4 == 0 && gmax_rows <= kInlineGmaxRows &&
+                              aligned16(row_gmax)),
+                "quant encode: per-row maxima outside the in-kernel reduction's limits");
     if (sel)
         quant_encode_kernel<DQ, true><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, scales_f32, scales_u8, gmax,
-                                                                     dq_out, codes, flags_reset, sel);
+                                                                     row_gmax, gmax_rows, dq_out, codes,
+                                                                     flags_reset, sel);
     else
         quant_encode_kernel<DQ, false><<<grid, kThreads, 0, stream>>>(x, n, vec_ok, scales_f32, scales_u8, gmax,
-                                                                      dq_out, codes, flags_reset, nullptr);
+                                                                      row_gmax, gmax_rows, dq_out, codes,
+                                                                      flags_reset, nullptr);
     BSQ_HIP(hipGetLastError());
 }
 }  // namespace
@@ -543,6 +574,11 @@ void launch_quant_encode_dq_rows(const float *x, uint64_t n, const float *row_gm
                                  hipStream_t stream, const uint8_t *sel) {
     BSQ_REQUIRE(n > 0 && rows > 0 && row_gmax && scales_u8 && codes && dq_out && gmax_scratch,
                 "quant encode: bad NF4_DQ arguments");
+    if (rows <= kInlineGmaxRows && rows % 4 == 0 && aligned16(row_gmax)) {
+        // few enough maxima: the encode's workgroups reduce them, no launch
+        encode_pass<true>(x, n, nullptr, scales_u8, nullptr, dq_out, codes, nullptr, sel, stream, row_gmax, rows);
+        return;
+    }
     rows_gmax_kernel<<<1, kThreads, 0, stream>>>(row_gmax, rows, gmax_scratch);
     BSQ_HIP(hipGetLastError());
     encode_pass<true>(x, n, nullptr, scales_u8, gmax_scratch, dq_out, codes, nullptr, sel, stream);

@@ -707,7 +707,10 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
             D.dense = nullptr;
             const bool dq = D.method == kMethodNF4DQ;
             timed_launch(kTimeDirectEncode, st, [&] {
-                if (dq) {
+                // the per-row maxima of a separation are reduced inside the
+                // pass when there are few enough of them
+                const bool inline_gmax = dq && have_row_gmax && rows <= kInlineGmaxRows && rows % 4 == 0;
+                if (dq && !inline_gmax) {
                     if (have_row_gmax) launch_rows_gmax(rt.d_row_gmax, rows, &rt.meta->gmax, st);
                     else launch_nf4dq_gmax(residual, N, D.codes, &rt.meta->gmax, st);
                 }
@@ -723,7 +726,12 @@ void compress_device(Runtime &rt, const float *d_in, bsq_device_packed_t *out, c
                 a.enc_codes = D.codes;
                 a.enc_scales_f32 = D.scales_f32;
                 a.enc_scales_u8 = D.scales_u8;
-                a.enc_gmax = &rt.meta->gmax;
+                if (inline_gmax) {
+                    a.enc_row_gmax = rt.d_row_gmax;
+                    a.enc_gmax_rows = rows;
+                } else {
+                    a.enc_gmax = &rt.meta->gmax;
+                }
                 a.enc_dq_out = &rt.meta->dq[SEC_DIRECT];
                 a.enc_sel = sel;
                 launch_topk_select(a, st);

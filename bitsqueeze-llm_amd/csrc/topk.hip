@@ -121,6 +121,7 @@ struct Shared {
     unsigned long long kt, kth;  // filter threshold, k-th largest composite key (fast path)
     float L[16];
     float wmax[kThreads / 64];  // per-wave maxima of the row's NF4_DQ block maxima
+    float gwmax[kThreads / 64];  // per-wave maxima of the per-row maxima (fused NF4_DQ encode)
 };
 
 // Fast path (row cached, k <= 256): at most this many candidates are ranked
@@ -547,12 +548,31 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     if constexpr (ENC) {
         nf4_level_table_build(etab);
         if constexpr (SRC == TopkSource::EncodeNF4DQ) {
-            const float raw = dq_raw_from_gmax(*a.enc_gmax);
-            dq = dq_effective(raw);
-            if (r == 0 && tid == 0) *a.enc_dq_out = raw;
+            if (!a.enc_row_gmax) {  // uniform
+                const float raw = dq_raw_from_gmax(*a.enc_gmax);
+                dq = dq_effective(raw);
+                if (r == 0 && tid == 0) *a.enc_dq_out = raw;
+            }
         }
     }
     __syncthreads();
+
+    // NF4_DQ's global scale from the separation's per-row maxima: this
+    // workgroup reduces them itself (max is order-free, so every workgroup
+    // gets the same bits), with the loads issued ahead of the row's so the
+    // reduction overlaps the row's memory round trip; no launch in between
+    constexpr int kGq = kInlineGmaxRows / (4 * kThreads);
+    f32x4 gq[kGq];
+    if constexpr (SRC == TopkSource::EncodeNF4DQ) {
+        if (a.enc_row_gmax) {  // uniform
+#pragma unroll
+            for (int j = 0; j < kGq; ++j) {
+                const uint32_t i4 = tid + kThreads * j;
+                gq[j] = 4 * i4 < a.enc_gmax_rows ? reinterpret_cast<const f32x4 *>(a.enc_row_gmax)[i4]
+                                                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    }
 
     const bool quad_ok = (SRC != TopkSource::DenseMinusNF4 && SRC != TopkSource::DenseMinusNF4DQ) ||
                          (reinterpret_cast<uintptr_t>(a.codes) & 1u) == 0;
@@ -583,6 +603,20 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         } else {
 #pragma unroll
             for (int u = 0; u < 4; ++u) v[m][u] = __builtin_nanf("");
+        }
+    }
+    if constexpr (SRC == TopkSource::EncodeNF4DQ) {
+        if (a.enc_row_gmax) {  // uniform
+            float gm = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kGq; ++j) gm = fmaxf(gm, fmaxf(fmaxf(gq[j].x, gq[j].y), fmaxf(gq[j].z, gq[j].w)));
+            for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+            if ((tid & 63) == 0) sh.gwmax[tid >> 6] = gm;
+            __syncthreads();
+            gm = fmaxf(fmaxf(sh.gwmax[0], sh.gwmax[1]), fmaxf(sh.gwmax[2], sh.gwmax[3]));
+            const float raw = dq_raw_from_gmax(__float_as_uint(gm));
+            dq = dq_effective(raw);
+            if (r == 0 && tid == 0) *a.enc_dq_out = raw;
         }
     }
     if constexpr (ENC) {
@@ -1183,8 +1217,13 @@ bool launch_topk_select(const TopkArgs &args, hipStream_t stream) {
             const bool dq = a.source == TopkSource::EncodeNF4DQ;
             BSQ_REQUIRE(topk_encode_supported(a.rows, a.cols, a.k, a.a, a.enc_codes) && !a.residual,
                         "top-k: shape outside the fused encode pass");
-            BSQ_REQUIRE(dq ? (a.enc_scales_u8 && a.enc_gmax && a.enc_dq_out) : (a.enc_scales_f32 != nullptr),
+            BSQ_REQUIRE(dq ? (a.enc_scales_u8 && (a.enc_gmax || a.enc_row_gmax) && a.enc_dq_out)
+                           : (a.enc_scales_f32 != nullptr),
                         "top-k: null encode output");
+            BSQ_REQUIRE(!a.enc_row_gmax || (dq && a.enc_gmax_rows > 0 && a.enc_gmax_rows % 4 == 0 &&
+                                            a.enc_gmax_rows <= kInlineGmaxRows &&
+                                            (reinterpret_cast<uintptr_t>(a.enc_row_gmax) & 15u) == 0),
+                        "top-k: per-row maxima outside the fused reduction's limits");
             const bool ok = dq ? try_launch_reg<TopkSource::EncodeNF4DQ>(a, stream)
                                : try_launch_reg<TopkSource::EncodeNF4>(a, stream);
             BSQ_REQUIRE(ok, "top-k: fused encode pass not launched");

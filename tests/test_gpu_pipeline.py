@@ -115,23 +115,33 @@ def test_direct_full_4096x11008_nf4dq_outlier_error():
     B.decompress_release()
 
 
-@pytest.mark.parametrize("rows,cols", [(48, 4096), (40, 1000), (16, 11008)])
-def test_nf4dq_global_scale_from_the_outlier_separation(rows, cols):
+@pytest.mark.parametrize("rows,cols,hot", [
+    (48, 4096, 24), (40, 1000, 20), (16, 11008, 8),
+    (42, 4096, 41),     # rows % 4 != 0: the maxima go through the reduce launch
+    (4096, 128, 4095),  # the most rows the encode kernels reduce themselves, largest in the last
+    (4096, 128, 2900),  # ... largest in the last of each lane's four loads
+    (4100, 128, 4099),  # more rows: the reduce launch
+])
+def test_nf4dq_global_scale_from_the_outlier_separation(rows, cols, hot):
     """The direct NF4_DQ section's global scale comes from the outlier
     separation kernel's per-row block maxima when cols % 64 == 0 (and from the
-    separate reduction otherwise): bytes and decode equal the oracle's with
-    all-zero blocks (which count as 1), NaN and infinity left in the residual
-    (sanitised to 0), and the largest block absmax in different rows."""
+    separate reduction otherwise), reduced inside the encode pass for up to
+    4096 rows (a multiple of 4) and by a reduce launch beyond: bytes and
+    decode equal the oracle's with all-zero blocks (which count as 1), NaN and
+    infinity left in the residual (sanitised to 0), and the largest block
+    absmax in row `hot`, through the fused encode + error pass and through
+    the encode alone (no error set)."""
     rng = np.random.default_rng(rows + cols)
     x = (rng.standard_normal((rows, cols)) * 0.01).astype(np.float32)
     x[0, :192] = 0.0                        # all-zero blocks in row 0
-    x[rows // 2] *= 500.0                    # the largest residual block sits in one row
+    x[hot] *= 500.0                          # the largest residual block sits in one row
     x[1, 5], x[2, 70] = np.nan, np.inf       # NaN is never an outlier; +inf is
     x[3, 9] = -np.inf
-    data, out, _ = run_direct(x, 0.01, 0.02, B.NF4_DQ)
-    exp_bytes, exp_out = oracle_direct(x, 0.01, 0.02, B.NF4_DQ)
-    assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
-    assert out.tobytes() == exp_out.tobytes()
+    for re in (0.02, 0.0):
+        data, out, _ = run_direct(x, 0.01, re, B.NF4_DQ)
+        exp_bytes, exp_out = oracle_direct(x, 0.01, re, B.NF4_DQ)
+        assert O.mask_pointer(data) == O.mask_pointer(exp_bytes)
+        assert out.tobytes() == exp_out.tobytes()
     # no outlier selection: the separate reduction
     data, out, _ = run_direct(x, 0.0, 0.02, B.NF4_DQ)
     exp_bytes, exp_out = oracle_direct(x, 0.0, 0.02, B.NF4_DQ)
