@@ -766,9 +766,13 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     if (total > kFastCap) {
         // fallback: exact threshold by radix select over the registers, on the
         // 32-bit key, then on the inverted column among equal keys
+        // (each pass re-derives the keys from the laundered row values:
+        // keys hoisted out of the pass loop would hold 4 NV4 more registers
+        // for the whole kernel, and cost the fast path its occupancy)
         uint32_t prefix = 0, mask = 0, remaining = k;
         for (int shift = 24; shift >= 0; shift -= 8) {
             sh.hist[tid] = 0;
+            (void)lane_id();
             __syncthreads();
 #pragma unroll
             for (int m = 0; m < NV4; ++m)
@@ -789,12 +793,13 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         uint32_t cpre = 0, cmask = 0;
         for (int shift = 8; shift >= 0; shift -= 8) {
             sh.hist[tid] = 0;
+            lt = lane_id();  // the inverted columns too: derived per pass, not held
             __syncthreads();
 #pragma unroll
             for (int m = 0; m < NV4; ++m)
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    const uint32_t inv = 0xFFFFu - (4 * (tid + kThreads * m) + u);
+                    const uint32_t inv = 0xFFFFu - (4 * (lt + kThreads * m) + u);
                     if (order_key(v[m][u]) == tkey && (inv & cmask) == cpre)
                         atomicAdd(&sh.hist[(inv >> shift) & 255u], 1u);
                     __builtin_amdgcn_sched_barrier(0);
