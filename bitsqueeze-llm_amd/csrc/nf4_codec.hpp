@@ -29,6 +29,25 @@ __device__ __noinline__ uint32_t nf4_code_scan(float v) {
     return best;
 }
 
+// The same scan over the levels held in `L` (LDS), inline and not unrolled:
+// a call to the out-of-line scan from a kernel that holds many values in
+// registers makes the compiler park them in callee-saved registers around
+// the call, which spreads them over far more registers than they need.
+__device__ __forceinline__ uint32_t nf4_code_scan_inline(const float *L, float v) {
+    if (!__builtin_isfinite(v)) v = 0.0f;
+    uint32_t best = 0;
+    float best_err = fabsf(v - L[0]);
+#pragma unroll 1
+    for (int i = 1; i < 16; ++i) {
+        const float err = fabsf(v - L[i]);
+        if (err < best_err) {
+            best_err = err;
+            best = static_cast<uint32_t>(i);
+        }
+    }
+    return best;
+}
+
 // Nearest NF4 code with the reference's tie rule: for |v| < 2 the scan's
 // answer is the number of exact decision thresholds at or below v, found
 // here with one table lookup and one comparison.  [-1, 1] is

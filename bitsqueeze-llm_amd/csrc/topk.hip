@@ -644,12 +644,9 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         for (int m = 0; m < NV4; ++m) {
             const uint32_t c4 = tid + kThreads * m;
             const bool inside = c4 < q4;
-            float sv[4], lm = 0.0f;
+            float lm = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                sv[u] = sanitize(v[m][u]);
-                lm = fmaxf(lm, fabsf(sv[u]));
-            }
+            for (int u = 0; u < 4; ++u) lm = fmaxf(lm, fabsf(sanitize(v[m][u])));
             const float bm = row16_max(lm);
             const float absmax = (bm > 0.0f) ? bm : 1.0f;
             float scale;
@@ -662,38 +659,42 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
                 scale = absmax;
             }
             const float inv = 1.0f / scale;
-            uint32_t c[4];
-            // |w| < 2 unless a block scale fell far below the block's absmax
-            // (an NF4_DQ scale code of 0 replaced by 1): the table path for
-            // the whole quad, the exact scan only for such quads
-            float w[4], lv[4];
-            bool small = true;
+            // |w| < 2 for the whole quad unless a block scale fell far below
+            // the block's absmax (an NF4_DQ scale code of 0 replaced by 1):
+            // rounding is monotone, so the quad's largest |w| is exactly
+            // fl(lm * inv); the table then, the exact scan only for such
+            // quads.  One value at a time (code packed as it comes, the value
+            // replaced by its error): few temporaries, so the row's registers
+            // leave room for more waves.
+            const bool small = lm * inv < 2.0f;
+            uint32_t packed = 0;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                w[u] = sv[u] * inv;
-                small = small && (fabsf(w[u]) < 2.0f);
-            }
-            if (small) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) c[u] = nf4_code_level_small(etab, w[u], lv[u]);
-            } else {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    c[u] = (fabsf(w[u]) < 2.0f) ? nf4_code_level_small(etab, w[u], lv[u]) : nf4_code_scan(w[u]);
-                    lv[u] = sh.L[c[u]];
+                const float w = sanitize(v[m][u]) * inv;
+                float lv;
+                uint32_t c;
+                if (small) {
+                    c = nf4_code_level_small(etab, w, lv);
+                } else {
+                    c = (fabsf(w) < 2.0f) ? nf4_code_level_small(etab, w, lv) : nf4_code_scan_inline(sh.L, w);
+                    lv = sh.L[c];
                 }
+                // element 2j in the high nibble: bytes (c0 c1) (c2 c3)
+                packed |= c << (8 * (u >> 1) + 4 * (1 - (u & 1)));
+                v[m][u] = inside ? v[m][u] - scale * lv : __builtin_nanf("");
+                // the error is formed here: left to the compiler, the
+                // subtraction sinks to the first later use and the levels
+                // and scales of every quad stay live until then
+                asm volatile("" : "+v"(v[m][u]));
             }
             const uint64_t e = row0 + 4ull * c4;
             if (inside) {
-                *reinterpret_cast<uint16_t *>(a.enc_codes + (e >> 1)) =
-                    static_cast<uint16_t>(((c[0] << 4) | c[1]) | (((c[2] << 4) | c[3]) << 8));
+                *reinterpret_cast<uint16_t *>(a.enc_codes + (e >> 1)) = static_cast<uint16_t>(packed);
                 if ((tid & 15u) == 0) {
                     if constexpr (SRC == TopkSource::EncodeNF4DQ) a.enc_scales_u8[e >> 6] = static_cast<uint8_t>(scode);
                     else a.enc_scales_f32[e >> 6] = scale;
                 }
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v[m][u] = inside ? v[m][u] - scale * lv[u] : __builtin_nanf("");
         }
     }
     // keys are recomputed from the values in every phase (an opaque copy of
