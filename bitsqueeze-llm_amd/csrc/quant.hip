@@ -173,16 +173,19 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
         for (int u = 0; u < kUnroll; ++u) {
             const uint64_t chunk = base + u * stride + threadIdx.x;
             const bool valid = chunk < nchunks;
+            // sanitised values (a selected entry reads as 0) and this lane's
+            // largest |value|
             if constexpr (SEL) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[u][i] = ((sb[u] >> i) & 1u) ? 0.0f : v[u][i];
             }
+            float lm = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[u][i] = sanitize(v[u][i]);
-            float m = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[u][i]));
-            m = group8_max(m);
+            for (int i = 0; i < 8; ++i) {
+                v[u][i] = sanitize(v[u][i]);
+                lm = fmaxf(lm, fabsf(v[u][i]));
+            }
+            const float m = group8_max(lm);
             const float absmax = (m > 0.0f) ? m : 1.0f;
             float scale;
             uint32_t scode = 0;
@@ -200,23 +203,18 @@ __global__ __launch_bounds__(kThreads) void quant_encode_kernel(
             }
             if (valid) {
                 // |v inv| < 2 (the table) unless a block scale fell far below
-                // the block's absmax (an NF4_DQ scale code of 0 replaced by 1):
-                // one test per chunk, the scan only for such chunks
-                float w[8];
-                bool small = true;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    w[i] = v[u][i] * inv;
-                    small = small && (fabsf(w[i]) < 2.0f);
-                }
+                // the block's absmax (an NF4_DQ scale code of 0 replaced by 1).
+                // Rounding is monotone, so the chunk's largest |v inv| is
+                // exactly fl(lm inv): one test per chunk; the per-element end
+                // test and the scan only for a chunk that needs them.
                 uint32_t c[8];
                 const uint64_t e0 = chunk * 8;
-                if (small) {
+                if (lm * inv < 2.0f && e0 + 8 <= n) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code_small(tab, w[i]) : 0u;  // odd tail: low nibble 0
+                    for (int i = 0; i < 8; ++i) c[i] = nf4_code_small(tab, v[u][i] * inv);
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code(tab, w[i]) : 0u;
+                    for (int i = 0; i < 8; ++i) c[i] = (e0 + i < n) ? nf4_code(tab, v[u][i] * inv) : 0u;  // odd tail: low nibble 0
                 }
                 store_codes(codes, n, chunk, vec_ok, c);
             }
@@ -524,15 +522,27 @@ void launch_rows_gmax(const float *row_gmax, uint32_t rows, uint32_t *gmax, hipS
 namespace {
 // one chunk per thread until the grid reaches its cap (small sections keep
 // every CU busy); the unrolled loop then covers the rest.  The cap is the
-// kernel's occupancy, five workgroups per CU (88 registers: five waves per
-// SIMD), so every workgroup is resident from the start: eight per CU ran as
-// a round of five and a round of three (supplement encode 54.5 -> 50.5 us).
+// variant's occupancy in workgroups per CU (five or six: 80 to 90
+// registers), so every workgroup is resident from the start: eight per CU
+// ran as a round of five and a round of three (supplement encode 54.5 ->
+// 50.5 us).
+template <bool DQ, bool SEL>
+unsigned encode_grid(uint64_t n) {
+    static const unsigned per_cu = [] {
+        int b = 0;
+        BSQ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &b, reinterpret_cast<const void *>(quant_encode_kernel<DQ, SEL>), kThreads, 0));
+        return static_cast<unsigned>(b > 0 ? b : 1);
+    }();
+    return grid_for(ceil_div(n, 8), per_cu);
+}
+
 template <bool DQ>
 void encode_pass(const float *x, uint64_t n, float *scales_f32, uint8_t *scales_u8, const uint32_t *gmax,
                  float *dq_out, uint8_t *codes, uint32_t *flags_reset, const uint8_t *sel, hipStream_t stream,
                  const float *row_gmax = nullptr, uint32_t gmax_rows = 0) {
     const bool vec_ok = aligned16(x) && ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
-    const unsigned grid = grid_for(ceil_div(n, 8), 5);
+    const unsigned grid = sel ? encode_grid<DQ, true>(n) : encode_grid<DQ, false>(n);
     BSQ_REQUIRE(!sel || n % kQuantBlock == 0, "quant encode: a selection bitmap needs whole blocks");
     BSQ_REQUIRE(!row_gmax || (DQ && gmax_rows > 0 && gmax_rows % 4 == 0 && gmax_rows <= kInlineGmaxRows &&
                               aligned16(row_gmax)),
