@@ -9,6 +9,7 @@ import os
 import re
 import struct
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -308,3 +309,14 @@ def test_consumer_links_the_nine_mangled_functions():
     assert all(m in undef for m in MANGLED[:9])
     dyn = subprocess.run(["readelf", "-d", CONSUMER], capture_output=True, text=True, check=True).stdout
     assert "libbitsqz_llm_lib.so.0" in dyn and os.path.join(INSTALL, "lib") in dyn
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 exits with status 2 and a
+    message that says so, before anything touches a device."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], cwd=root,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in (r.stdout + r.stderr)
+    assert r.stdout.strip() == ""  # no JSON line
