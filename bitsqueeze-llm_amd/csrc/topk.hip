@@ -524,6 +524,10 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
     __shared__ float bv[kFastCap];
     // the row's selected columns, one bit each (separation: residual, bitmap)
     __shared__ uint32_t rowbits[NV4 * 32];
+    // encode sources: each wave's block maxima and (scale, +-1 / scale) per
+    // block, slot 4 m + (lane / 16) % 4 (unused, and dropped, otherwise)
+    __shared__ float enc_bmax[kThreads / 64][4 * NV4];
+    __shared__ float2 enc_scl[kThreads / 64][4 * NV4];
     const uint32_t cols = a.cols, k = a.k, q4 = cols / 4;
     const uint32_t r = blockIdx.x, tid = threadIdx.x;
     const uint64_t row0 = static_cast<uint64_t>(r) * cols;
@@ -640,14 +644,25 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
         // raw value, as the DenseMinusNF4(DQ) sources compute it from the
         // stored encoding.  Padding rows (whole DPP rows past the row end)
         // store nothing and stay NaN.
+        //
+        // The scale of a block is the same in its 16 lanes, and its chain
+        // (NF4_DQ: a division, the E4M3 encode and decode; then 1 / scale)
+        // costs the same issue slots whether one lane needs it or 64.  So
+        // the wave's 4 NV4 block maxima go to LDS (slot 4 m + block of the
+        // DPP row), one lane per block runs the chain once for all of them,
+        // and the quads read their block's scale back.
+        const int g = static_cast<int>((tid >> 4) & 3u), wv = static_cast<int>(tid >> 6), wl = static_cast<int>(tid & 63u);
 #pragma unroll
         for (int m = 0; m < NV4; ++m) {
-            const uint32_t c4 = tid + kThreads * m;
-            const bool inside = c4 < q4;
             float lm = 0.0f;
 #pragma unroll
             for (int u = 0; u < 4; ++u) lm = fmaxf(lm, fabsf(sanitize(v[m][u])));
             const float bm = row16_max(lm);
+            if ((tid & 15u) == 0) enc_bmax[wv][4 * m + g] = bm;
+        }
+        __syncthreads();
+        if (wl < 4 * NV4) {
+            const float bm = enc_bmax[wv][wl];
             const float absmax = (bm > 0.0f) ? bm : 1.0f;
             float scale;
             uint32_t scode = 0;
@@ -659,14 +674,26 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
                 scale = absmax;
             }
             const float inv = 1.0f / scale;
-            // |w| < 2 for the whole quad unless a block scale fell far below
-            // the block's absmax (an NF4_DQ scale code of 0 replaced by 1):
-            // rounding is monotone, so the quad's largest |w| is exactly
-            // fl(lm * inv); the table then, the exact scan only for such
-            // quads.  One value at a time (code packed as it comes, the value
-            // replaced by its error): few temporaries, so the row's registers
-            // leave room for more waves.
-            const bool small = lm * inv < 2.0f;
+            // |w| < 2 in the whole block unless its scale fell far below its
+            // absmax (an NF4_DQ scale code of 0 replaced by 1); rounding is
+            // monotone, so the block's largest |w| is exactly fl(bm * inv).
+            // The flag rides in the sign of inv (> 0).
+            enc_scl[wv][wl] = float2{scale, (bm * inv < 2.0f) ? inv : -inv};
+            const uint32_t c4b = static_cast<uint32_t>(64 * wv + 16 * (wl & 3) + kThreads * (wl >> 2));
+            if (c4b < q4) {
+                const uint64_t blk = (row0 + 4ull * c4b) >> 6;
+                if constexpr (SRC == TopkSource::EncodeNF4DQ) a.enc_scales_u8[blk] = static_cast<uint8_t>(scode);
+                else a.enc_scales_f32[blk] = scale;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < NV4; ++m) {
+            const uint32_t c4 = tid + kThreads * m;
+            const bool inside = c4 < q4;
+            const float2 sc = enc_scl[wv][4 * m + g];
+            const float scale = sc.x, inv = fabsf(sc.y);
+            const bool small = sc.y > 0.0f;  // the table for the whole block
             uint32_t packed = 0;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -687,13 +714,9 @@ __global__ __launch_bounds__(kThreads) void topk_reg_kernel(TopkArgs a) {
                 // and scales of every quad stay live until then
                 asm volatile("" : "+v"(v[m][u]));
             }
-            const uint64_t e = row0 + 4ull * c4;
             if (inside) {
+                const uint64_t e = row0 + 4ull * c4;
                 *reinterpret_cast<uint16_t *>(a.enc_codes + (e >> 1)) = static_cast<uint16_t>(packed);
-                if ((tid & 15u) == 0) {
-                    if constexpr (SRC == TopkSource::EncodeNF4DQ) a.enc_scales_u8[e >> 6] = static_cast<uint8_t>(scode);
-                    else a.enc_scales_f32[e >> 6] = scale;
-                }
             }
         }
     }
